@@ -1,0 +1,738 @@
+// C-ABI implementation of libgustann_hip.so (declared in include/gustann.h).
+//
+// Host orchestration of the in-memory search path: the GustANN facade and the
+// PURE_MEM executor of the reference (src/ssd_search.cu, src/pure_mem.cu),
+// the PQ loader/uploader (src/pq_search.cu) and the nav-graph loader
+// (src/nav_graph.cu), with device residency, validation and error codes in
+// place of the reference's exit()/abort()/throw.
+#include "../../include/gustann.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "formats.hpp"
+#include "gann_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Error {
+  int code;
+  std::string msg;
+};
+
+#define GANN_HIP(expr)                                                                         \
+  do {                                                                                         \
+    hipError_t e_ = (expr);                                                                    \
+    if (e_ != hipSuccess)                                                                      \
+      throw Error{e_ == hipErrorOutOfMemory ? GANN_ERR_NOMEM : GANN_ERR_HIP,                   \
+                  std::string(#expr) + ": " + hipGetErrorString(e_)};                          \
+  } while (0)
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    return GANN_OK;
+  } catch (const Error& e) {
+    g_err = e.msg;
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    g_err = "host allocation failed";
+    return GANN_ERR_NOMEM;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return GANN_ERR_INVALID;
+  } catch (...) {
+    g_err = "unknown error";
+    return GANN_ERR_INVALID;
+  }
+}
+
+[[noreturn]] void raise(int code, const std::string& msg) { throw Error{code, msg}; }
+
+// Device allocation owned by RAII.
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  void ensure(size_t n) {
+    if (n <= bytes && p) return;
+    release();
+    GANN_HIP(hipMalloc(&p, n ? n : 1));
+    bytes = n;
+  }
+  template <class T>
+  T* as() const {
+    return reinterpret_cast<T*>(p);
+  }
+};
+
+struct PinnedBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  PinnedBuf() = default;
+  PinnedBuf(const PinnedBuf&) = delete;
+  PinnedBuf& operator=(const PinnedBuf&) = delete;
+  ~PinnedBuf() {
+    if (p) (void)hipHostFree(p);
+  }
+  void alloc(size_t n) {
+    GANN_HIP(hipHostMalloc(&p, n ? n : 1, hipHostMallocMapped | hipHostMallocPortable));
+    bytes = n;
+  }
+};
+
+void upload(DevBuf& d, const void* src, size_t bytes) {
+  d.ensure(bytes);
+  if (bytes) GANN_HIP(hipMemcpy(d.p, src, bytes, hipMemcpyHostToDevice));
+}
+
+double now_s() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+unsigned host_threads() {
+  unsigned t = std::thread::hardware_concurrency();
+  return t == 0 ? 4 : std::min(t, 16u);
+}
+
+// Checks every node record of a block of pages: deg <= R, neighbour ids
+// < num_pts, no id twice in one list.  The reference does not check
+// (src/impl/pure_mem.cuh:288-301 indexes with whatever the file holds); the
+// kernels index the code table with these ids, so they are validated once here.
+void validate_pages(const gann::DiskLayout& L, const uint8_t* pages, int64_t first_page,
+                    int64_t npages, std::atomic<int64_t>* bad_node) {
+  int64_t u0 = first_page * L.nodes_per_page;
+  int64_t u1 = std::min(L.num_pts, (first_page + npages) * L.nodes_per_page);
+  unsigned nt = host_threads();
+  std::vector<std::thread> th;
+  for (unsigned t = 0; t < nt; ++t) {
+    th.emplace_back([&, t] {
+      std::vector<uint32_t> tmp((size_t)L.max_m);
+      for (int64_t u = u0 + t; u < u1; u += nt) {
+        if (bad_node->load(std::memory_order_relaxed) >= 0) return;
+        const uint8_t* rec = pages + (u / L.nodes_per_page - first_page) * gann::kSectorBytes +
+                             (u % L.nodes_per_page) * L.node_len;
+        int32_t deg;
+        std::memcpy(&deg, rec + L.data_len, 4);
+        bool ok = deg >= 0 && deg <= L.max_m;
+        if (ok) {
+          std::memcpy(tmp.data(), rec + L.data_len + 4, (size_t)deg * 4);
+          for (int32_t j = 0; j < deg && ok; ++j) ok = tmp[(size_t)j] < (uint64_t)L.num_pts;
+          if (ok) {
+            std::sort(tmp.begin(), tmp.begin() + deg);
+            ok = std::adjacent_find(tmp.begin(), tmp.begin() + deg) == tmp.begin() + deg;
+          }
+        }
+        if (!ok) {
+          int64_t expect = -1;
+          bad_node->compare_exchange_strong(expect, u);
+          return;
+        }
+      }
+    });
+  }
+  for (auto& x : th) x.join();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- PQ object
+
+struct gann_pq {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  gann::PQDev dev{};
+  DevBuf pivots_t, centroid, chunk_off, codes;
+  bool codes_borrowed = false;
+  // scratch of the host-pointer entry points
+  DevBuf q, ids, out;
+
+  ~gann_pq() {
+    if (stream) {
+      (void)hipSetDevice(device);
+      (void)hipStreamDestroy(stream);
+    }
+  }
+
+  // Uploads pivots (transposed to [dim][256] as src/pq_search.cu:88-93),
+  // centroid and chunk offsets.
+  void upload_static(const float* pivots, const float* c, const int32_t* off, int dim, int M) {
+    std::vector<float> pt((size_t)dim * gann::kNumPivots);
+    for (int i = 0; i < gann::kNumPivots; ++i)
+      for (int j = 0; j < dim; ++j) pt[(size_t)j * gann::kNumPivots + i] = pivots[(size_t)i * dim + j];
+    upload(pivots_t, pt.data(), pt.size() * 4);
+    upload(centroid, c, (size_t)dim * 4);
+    upload(chunk_off, off, (size_t)(M + 1) * 4);
+    dev.dim = dim;
+    dev.M = M;
+    dev.pivots_t = pivots_t.as<float>();
+    dev.centroid = centroid.as<float>();
+    dev.chunk_off = chunk_off.as<int32_t>();
+  }
+};
+
+namespace {
+
+void check_chunks(const int32_t* off, int dim, int M) {
+  if (M < 1 || dim < 1) raise(GANN_ERR_INVALID, "pq: need dim >= 1 and num_chunks >= 1");
+  if (off[0] != 0 || off[M] != dim)
+    raise(GANN_ERR_FORMAT, "pq chunk offsets must start at 0 and end at dim");
+  for (int m = 0; m < M; ++m)
+    if (off[m + 1] < off[m]) raise(GANN_ERR_FORMAT, "pq chunk offsets must be non-decreasing");
+}
+
+void check_lds(size_t bytes, int device, const char* what) {
+  int lim = 0;
+  GANN_HIP(hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+  if (bytes > (size_t)lim)
+    raise(GANN_ERR_UNSUPPORTED, std::string(what) + ": LDS footprint " + std::to_string(bytes) +
+                                    " B exceeds the device limit " + std::to_string(lim) + " B");
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- handle
+
+struct gann_handle {
+  int device = 0;
+  int dtype = 0;
+  int placement = GANN_PLACEMENT_HBM;
+  hipStream_t stream = nullptr;
+  gann::DiskLayout layout;
+  gann_pq pq;
+  // pages: HBM copy or pinned host memory
+  DevBuf pages_dev;
+  PinnedBuf pages_host;
+  gann::IndexDev ix{};
+  // pivot graph
+  bool has_nav = false;
+  gann::NavHost nav_host_meta;  // sizes only (data vectors released after upload)
+  DevBuf nav_data, nav_graph, nav_map;
+  gann::NavDev nav{};
+  // per-call scratch
+  DevBuf q, entries, local, nns, dists, found, nexp, nadc, counters;
+  DevBuf luts, lists, state;
+  PinnedBuf counter_host;
+
+  ~gann_handle() {
+    if (stream) {
+      (void)hipSetDevice(device);
+      (void)hipStreamDestroy(stream);
+    }
+  }
+};
+
+namespace {
+
+void open_handle(const gann_config* cfg, gann_handle* h) {
+  if (!cfg || !cfg->index_file || !cfg->pq_prefix || !*cfg->pq_prefix)
+    raise(GANN_ERR_INVALID, "config needs index_file and pq_prefix (src/ssd_search.cu:59-67)");
+  if (cfg->dtype != GANN_UINT8 && cfg->dtype != GANN_FLOAT) raise(GANN_ERR_INVALID, "unknown dtype");
+  if (cfg->placement != GANN_PLACEMENT_HBM && cfg->placement != GANN_PLACEMENT_HOST_PINNED)
+    raise(GANN_ERR_INVALID, "unknown placement");
+  int ndev = 0;
+  GANN_HIP(hipGetDeviceCount(&ndev));
+  if (cfg->device_id < 0 || cfg->device_id >= ndev) raise(GANN_ERR_INVALID, "device_id out of range");
+  h->device = cfg->device_id;
+  h->dtype = cfg->dtype;
+  h->placement = cfg->placement;
+  GANN_HIP(hipSetDevice(h->device));
+  GANN_HIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+  h->pq.device = h->device;
+  GANN_HIP(hipStreamCreateWithFlags(&h->pq.stream, hipStreamNonBlocking));
+
+  std::string err;
+  const int64_t es = cfg->dtype == GANN_UINT8 ? 1 : 4;
+  if (!gann::parse_disk_meta(cfg->index_file, es, &h->layout, &err))
+    raise(err.rfind("cannot open", 0) == 0 ? GANN_ERR_IO : GANN_ERR_FORMAT, err);
+  const gann::DiskLayout& L = h->layout;
+
+  // PQ (src/ssd_search.cu:59-67, src/pq_search.cu:56-121)
+  {
+    gann::PQHost pqh;
+    std::string pp = std::string(cfg->pq_prefix);
+    if (!gann::read_pq(pp + "_pivots.bin", pp + "_compressed.bin", &pqh, true, &err))
+      raise(err.rfind("cannot open", 0) == 0 ? GANN_ERR_IO : GANN_ERR_FORMAT, err);
+    if (pqh.dim != L.dim) raise(GANN_ERR_FORMAT, "pq dim differs from the index dim");  // :124
+    if (pqh.num_pts != L.num_pts)
+      raise(GANN_ERR_FORMAT, "pq point count differs from the index");  // :125
+    check_chunks(pqh.chunk_offsets.data(), pqh.dim, pqh.num_chunks);
+    h->pq.upload_static(pqh.pivots.data(), pqh.centroid.data(), pqh.chunk_offsets.data(), pqh.dim,
+                        pqh.num_chunks);
+    upload(h->pq.codes, pqh.codes.data(), pqh.codes.size());
+    h->pq.dev.codes = h->pq.codes.as<uint8_t>();
+    h->pq.dev.num_pts = pqh.num_pts;
+  }
+
+  // pivot graph (src/ssd_search.cu:70-78, src/nav_graph.cu:41-100)
+  if (cfg->nav_prefix && *cfg->nav_prefix) {
+    gann::NavHost nh;
+    if (!gann::read_nav(cfg->nav_prefix, es, &nh, &err))
+      raise(err.rfind("cannot open", 0) == 0 ? GANN_ERR_IO : GANN_ERR_FORMAT, err);
+    if (nh.dim != L.dim) raise(GANN_ERR_FORMAT, "nav_index.data dim differs from the index dim");
+    upload(h->nav_data, nh.data.data(), nh.data.size());
+    upload(h->nav_graph, nh.graph.data(), nh.graph.size() * 4);
+    upload(h->nav_map, nh.mapping.data(), nh.mapping.size() * 4);
+    h->has_nav = true;
+    h->nav_host_meta.num_node = nh.num_node;
+    h->nav_host_meta.dim = nh.dim;
+    h->nav_host_meta.max_m = nh.max_m;
+    h->nav_host_meta.start = nh.start;
+    h->nav = gann::NavDev{h->nav_data.as<uint8_t>(), h->nav_graph.as<int32_t>(),
+                          h->nav_map.as<int32_t>(), nh.num_node, nh.max_m, nh.start};
+  }
+
+  // pages (src/pure_mem.cu:45-69): read through a pinned staging ring into
+  // HBM, or keep them in pinned host memory for the zero-copy placement.
+  const int64_t total = L.num_pages * gann::kSectorBytes;
+  std::atomic<int64_t> bad{-1};
+  gann::File f(cfg->index_file, "rb");
+  if (!f || !f.seek(gann::kSectorBytes)) raise(GANN_ERR_IO, "cannot read index pages");
+  if (cfg->placement == GANN_PLACEMENT_HOST_PINNED) {
+    h->pages_host.alloc((size_t)total);
+    const int64_t chunk_pages = 65536;  // 256 MiB
+    for (int64_t p0 = 0; p0 < L.num_pages; p0 += chunk_pages) {
+      int64_t np = std::min(chunk_pages, L.num_pages - p0);
+      uint8_t* dst = (uint8_t*)h->pages_host.p + p0 * gann::kSectorBytes;
+      if (!f.read(dst, (size_t)(np * gann::kSectorBytes))) raise(GANN_ERR_FORMAT, "short read of index pages");
+      validate_pages(L, dst, p0, np, &bad);
+    }
+    void* dptr = nullptr;
+    GANN_HIP(hipHostGetDevicePointer(&dptr, h->pages_host.p, 0));
+    h->ix.pages = (const uint8_t*)dptr;
+  } else {
+    h->pages_dev.ensure((size_t)total);
+    const int64_t chunk_pages = 16384;  // 64 MiB per staging buffer
+    PinnedBuf stage[2];
+    stage[0].alloc((size_t)(chunk_pages * gann::kSectorBytes));
+    stage[1].alloc((size_t)(chunk_pages * gann::kSectorBytes));
+    hipEvent_t done[2];
+    bool recorded[2] = {false, false};
+    GANN_HIP(hipEventCreate(&done[0]));
+    GANN_HIP(hipEventCreate(&done[1]));
+    int k = 0;
+    for (int64_t p0 = 0; p0 < L.num_pages; p0 += chunk_pages, k ^= 1) {
+      int64_t np = std::min(chunk_pages, L.num_pages - p0);
+      if (recorded[k]) GANN_HIP(hipEventSynchronize(done[k]));
+      uint8_t* buf = (uint8_t*)stage[k].p;
+      if (!f.read(buf, (size_t)(np * gann::kSectorBytes))) raise(GANN_ERR_FORMAT, "short read of index pages");
+      validate_pages(L, buf, p0, np, &bad);
+      GANN_HIP(hipMemcpyAsync((uint8_t*)h->pages_dev.p + p0 * gann::kSectorBytes, buf,
+                              (size_t)(np * gann::kSectorBytes), hipMemcpyHostToDevice, h->stream));
+      GANN_HIP(hipEventRecord(done[k], h->stream));
+      recorded[k] = true;
+    }
+    GANN_HIP(hipStreamSynchronize(h->stream));
+    (void)hipEventDestroy(done[0]);
+    (void)hipEventDestroy(done[1]);
+    h->ix.pages = h->pages_dev.as<uint8_t>();
+  }
+  if (bad.load() >= 0)
+    raise(GANN_ERR_FORMAT, "node record " + std::to_string(bad.load()) +
+                               ": degree > R, neighbour id out of range or repeated");
+  h->ix.nodes_per_page = L.nodes_per_page;
+  h->ix.node_len = L.node_len;
+  h->ix.data_len = L.data_len;
+  h->ix.num_pts = L.num_pts;
+  h->ix.medoid = L.medoid;
+  h->ix.R = (int32_t)L.max_m;
+  h->ix.dim = (int32_t)L.dim;
+  h->counter_host.alloc(64);
+}
+
+void validate_search(const gann_handle* h, int32_t nq, int32_t topk, int32_t L, int32_t beam) {
+  if (nq < 0) raise(GANN_ERR_INVALID, "nq must be >= 0");
+  if (topk < 1) raise(GANN_ERR_INVALID, "topk must be >= 1");
+  if (L < topk) raise(GANN_ERR_INVALID, "L (ef_search) must be >= topk (bin/search_disk.cpp:189-192)");
+  if (beam != 1) raise(GANN_ERR_UNSUPPORTED, "beam_width must be 1 (one node per iteration)");
+  if (h->layout.max_m > 64)
+    raise(GANN_ERR_UNSUPPORTED, "graph degree R > 64 is not supported by the wave64 kernels");
+}
+
+// Entry selection (src/pure_mem.cu:104-124): nav kernel + on-device
+// translation, or the medoid.
+void run_entries(gann_handle* h, const float* q_dev, int32_t nq, int32_t* entries, int32_t* local,
+                 int32_t* fallback, hipStream_t s) {
+  if (h->has_nav) {
+    GANN_HIP(gann::launch_fill_i32(fallback, 1, 0, s));
+    GANN_HIP(gann::launch_nav_entry(h->nav, h->dtype, h->layout.medoid, h->layout.num_pts,
+                                    (int)h->layout.dim, q_dev, nq, entries, local, fallback, s));
+  } else {
+    GANN_HIP(gann::launch_fill_i32(entries, nq, (int32_t)h->layout.medoid, s));
+    if (local) GANN_HIP(gann::launch_fill_i32(local, nq, -1, s));
+    GANN_HIP(gann::launch_fill_i32(fallback, 1, 0, s));
+  }
+}
+
+void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                int32_t mode, const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
+                int32_t* nexp, int32_t* nadc, hipStream_t s) {
+  const gann::DiskLayout& Ly = h->layout;
+  if (mode == GANN_MODE_FUSED) {
+    check_lds(gann::search_smem_bytes(h->pq.dev.M, (int)Ly.dim, L, (int)Ly.max_m, topk), h->device,
+              "fused search");
+    GANN_HIP(gann::launch_search(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,
+                                 dists, found, nexp, nadc, s));
+    return;
+  }
+  if (mode != GANN_MODE_STEPWISE) raise(GANN_ERR_INVALID, "unknown mode");
+  // step-wise: LUTs in HBM, one launch per expansion round, host polls the
+  // active count (the request[] round trip of src/hyd_task_runner.cu:126-178)
+  const int64_t cap = L + Ly.max_m;
+  h->luts.ensure((size_t)nq * h->pq.dev.M * gann::kNumPivots * 4);
+  h->lists.ensure((size_t)nq * cap * 8);
+  h->state.ensure((size_t)nq * gann::step_state_bytes());
+  h->counters.ensure(64);
+  GANN_HIP(gann::launch_step_init(h->pq.dev, q_dev, nq, entries, h->luts.as<float>(), h->state.p, s));
+  int32_t* active = h->counters.as<int32_t>() + 1;
+  GANN_HIP(gann::launch_fill_i32(active, 1, nq, s));
+  int32_t* host_active = (int32_t*)h->counter_host.p;
+  const int64_t max_rounds = Ly.num_pts + 2;
+  const int rounds_per_poll = 8;
+  for (int64_t r = 0; r < max_rounds; r += rounds_per_poll) {
+    for (int k = 0; k < rounds_per_poll; ++k)
+      GANN_HIP(gann::launch_step_round(h->ix, h->pq.dev, h->dtype, q_dev, nq, h->luts.as<float>(),
+                                       topk, L, h->lists.as<uint64_t>(), h->state.p, nns, dists,
+                                       active, s));
+    GANN_HIP(hipMemcpyAsync(host_active, active, 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipStreamSynchronize(s));
+    if (*host_active <= 0) break;
+  }
+  GANN_HIP(gann::launch_step_finish(nq, topk, h->state.p, nns, dists, found, nexp, nadc, s));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gann_last_error(void) { return g_err.c_str(); }
+const char* gann_version(void) { return "gustann-mi355x 0.1 (gfx950)"; }
+
+int gann_open(const gann_config* cfg, gann_handle** out) {
+  if (!out) {
+    g_err = "out is NULL";
+    return GANN_ERR_INVALID;
+  }
+  *out = nullptr;
+  gann_handle* h = nullptr;
+  int rc = guarded([&] {
+    h = new gann_handle();
+    open_handle(cfg, h);
+  });
+  if (rc != GANN_OK) {
+    delete h;
+    return rc;
+  }
+  *out = h;
+  return GANN_OK;
+}
+
+int gann_close(gann_handle* h) {
+  if (!h) return GANN_OK;
+  return guarded([&] {
+    GANN_HIP(hipSetDevice(h->device));
+    delete h;
+  });
+}
+
+int gann_get_info(const gann_handle* h, gann_index_info* info) {
+  if (!h || !info) {
+    g_err = "NULL argument";
+    return GANN_ERR_INVALID;
+  }
+  const gann::DiskLayout& L = h->layout;
+  info->num_pts = L.num_pts;
+  info->dim = L.dim;
+  info->medoid = L.medoid;
+  info->max_m = L.max_m;
+  info->node_len = L.node_len;
+  info->nodes_per_page = L.nodes_per_page;
+  info->num_pages = L.num_pages;
+  info->dtype = h->dtype;
+  info->num_chunks = h->pq.dev.M;
+  info->nav_num_node = h->has_nav ? h->nav_host_meta.num_node : 0;
+  info->nav_max_m = h->has_nav ? h->nav_host_meta.max_m : 0;
+  info->nav_start = h->has_nav ? h->nav_host_meta.start : 0;
+  return GANN_OK;
+}
+
+int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int32_t L,
+                   int32_t beam_width, int32_t mode, int32_t* nns, float* dists,
+                   int32_t* found_cnt, int32_t* n_exp, gann_stats* st) {
+  return guarded([&] {
+    if (!h) raise(GANN_ERR_INVALID, "handle is NULL");
+    validate_search(h, nq, topk, L, beam_width);
+    if (st) *st = gann_stats{};
+    if (nq == 0) return;
+    if (!q || !nns || !dists || !found_cnt) raise(GANN_ERR_INVALID, "NULL buffer");
+    GANN_HIP(hipSetDevice(h->device));
+    const int64_t D = h->layout.dim;
+    hipStream_t s = h->stream;
+    h->q.ensure((size_t)nq * D * 4);
+    h->entries.ensure((size_t)nq * 4);
+    h->nns.ensure((size_t)nq * topk * 4);
+    h->dists.ensure((size_t)nq * topk * 4);
+    h->found.ensure((size_t)nq * 4);
+    h->nexp.ensure((size_t)nq * 4);
+    h->nadc.ensure((size_t)nq * 4);
+    h->counters.ensure(64);
+    // query upload is outside the timed scope (src/pure_mem.cu:78-79)
+    GANN_HIP(hipMemcpyAsync(h->q.p, q, (size_t)nq * D * 4, hipMemcpyHostToDevice, s));
+    GANN_HIP(hipStreamSynchronize(s));
+    const double t0 = now_s();
+    run_entries(h, h->q.as<float>(), nq, h->entries.as<int32_t>(), nullptr, h->counters.as<int32_t>(), s);
+    GANN_HIP(hipStreamSynchronize(s));
+    const double t1 = now_s();
+    run_search(h, h->q.as<float>(), nq, topk, L, mode, h->entries.as<int32_t>(), h->nns.as<int32_t>(),
+               h->dists.as<float>(), h->found.as<int32_t>(), h->nexp.as<int32_t>(),
+               h->nadc.as<int32_t>(), s);
+    GANN_HIP(hipStreamSynchronize(s));
+    const double t2 = now_s();
+    GANN_HIP(hipMemcpyAsync(nns, h->nns.p, (size_t)nq * topk * 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipMemcpyAsync(dists, h->dists.p, (size_t)nq * topk * 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipMemcpyAsync(found_cnt, h->found.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s));
+    std::vector<int32_t> ne((size_t)nq), na((size_t)nq);
+    int32_t fb = 0;
+    GANN_HIP(hipMemcpyAsync(ne.data(), h->nexp.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipMemcpyAsync(na.data(), h->nadc.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipMemcpyAsync(&fb, h->counters.p, 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipStreamSynchronize(s));
+    if (n_exp) std::memcpy(n_exp, ne.data(), (size_t)nq * 4);
+    if (st) {
+      st->run_time_s = t2 - t0;
+      st->entry_time_s = t1 - t0;
+      int64_t e = 0, a = 0;
+      for (int32_t i = 0; i < nq; ++i) {
+        e += ne[(size_t)i];
+        a += na[(size_t)i];
+      }
+      st->n_expansions = e;
+      st->n_adc = a;
+      const double rec = (double)h->layout.data_len + 4.0;
+      st->alg_bytes = (double)e * rec + (double)a * (4.0 + h->pq.dev.M) +
+                      (double)nq * (4.0 * (double)D + 8.0 * topk);
+      st->n_nav_fallback = fb;
+    }
+  });
+}
+
+int gann_search(gann_handle* h, const float* q, int32_t nq, int32_t topk, int32_t L,
+                int32_t beam_width, int32_t* nns, float* dists, int32_t* found_cnt,
+                gann_stats* st) {
+  return gann_search_ex(h, q, nq, topk, L, beam_width, GANN_MODE_FUSED, nns, dists, found_cnt,
+                        nullptr, st);
+}
+
+int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                       int32_t* entries_dev, int32_t* nns_dev, float* dists_dev,
+                       int32_t* found_dev, int32_t* n_exp_dev, int32_t* n_adc_dev, void* stream) {
+  return guarded([&] {
+    if (!h) raise(GANN_ERR_INVALID, "handle is NULL");
+    validate_search(h, nq, topk, L, 1);
+    if (nq == 0) return;
+    if (!q_dev || !entries_dev || !nns_dev || !dists_dev || !found_dev)
+      raise(GANN_ERR_INVALID, "NULL buffer");
+    GANN_HIP(hipSetDevice(h->device));
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    h->counters.ensure(64);
+    run_entries(h, q_dev, nq, entries_dev, nullptr, h->counters.as<int32_t>(), s);
+    run_search(h, q_dev, nq, topk, L, GANN_MODE_FUSED, entries_dev, nns_dev, dists_dev, found_dev,
+               n_exp_dev, n_adc_dev, s);
+  });
+}
+
+int gann_nav_entry(gann_handle* h, const float* q, int32_t nq, int32_t* entries_out,
+                   int32_t* local_out) {
+  return guarded([&] {
+    if (!h) raise(GANN_ERR_INVALID, "handle is NULL");
+    if (nq < 0) raise(GANN_ERR_INVALID, "nq must be >= 0");
+    if (nq == 0) return;
+    if (!q || !entries_out) raise(GANN_ERR_INVALID, "NULL buffer");
+    GANN_HIP(hipSetDevice(h->device));
+    hipStream_t s = h->stream;
+    const int64_t D = h->layout.dim;
+    h->q.ensure((size_t)nq * D * 4);
+    h->entries.ensure((size_t)nq * 4);
+    h->local.ensure((size_t)nq * 4);
+    h->counters.ensure(64);
+    GANN_HIP(hipMemcpyAsync(h->q.p, q, (size_t)nq * D * 4, hipMemcpyHostToDevice, s));
+    run_entries(h, h->q.as<float>(), nq, h->entries.as<int32_t>(), h->local.as<int32_t>(),
+                h->counters.as<int32_t>(), s);
+    GANN_HIP(hipMemcpyAsync(entries_out, h->entries.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s));
+    if (local_out)
+      GANN_HIP(hipMemcpyAsync(local_out, h->local.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipStreamSynchronize(s));
+  });
+}
+
+// ---------------------------------------------------------------- PQ entry points
+
+int gann_pq_open(const char* pq_prefix, int32_t device_id, gann_pq** out) {
+  if (!out) {
+    g_err = "out is NULL";
+    return GANN_ERR_INVALID;
+  }
+  *out = nullptr;
+  gann_pq* p = nullptr;
+  int rc = guarded([&] {
+    if (!pq_prefix || !*pq_prefix) raise(GANN_ERR_INVALID, "pq_prefix is empty");
+    int ndev = 0;
+    GANN_HIP(hipGetDeviceCount(&ndev));
+    if (device_id < 0 || device_id >= ndev) raise(GANN_ERR_INVALID, "device_id out of range");
+    GANN_HIP(hipSetDevice(device_id));
+    p = new gann_pq();
+    p->device = device_id;
+    GANN_HIP(hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking));
+    gann::PQHost pqh;
+    std::string err, pp(pq_prefix);
+    if (!gann::read_pq(pp + "_pivots.bin", pp + "_compressed.bin", &pqh, true, &err))
+      raise(err.rfind("cannot open", 0) == 0 ? GANN_ERR_IO : GANN_ERR_FORMAT, err);
+    check_chunks(pqh.chunk_offsets.data(), pqh.dim, pqh.num_chunks);
+    p->upload_static(pqh.pivots.data(), pqh.centroid.data(), pqh.chunk_offsets.data(), pqh.dim,
+                     pqh.num_chunks);
+    upload(p->codes, pqh.codes.data(), pqh.codes.size());
+    p->dev.codes = p->codes.as<uint8_t>();
+    p->dev.num_pts = pqh.num_pts;
+  });
+  if (rc != GANN_OK) {
+    delete p;
+    return rc;
+  }
+  *out = p;
+  return GANN_OK;
+}
+
+int gann_pq_create(const float* pivots, const float* centroid, const int32_t* chunk_offsets,
+                   int32_t dim, int32_t num_chunks, const uint8_t* codes, int64_t num_pts,
+                   int32_t codes_on_device, int32_t device_id, gann_pq** out) {
+  if (!out) {
+    g_err = "out is NULL";
+    return GANN_ERR_INVALID;
+  }
+  *out = nullptr;
+  gann_pq* p = nullptr;
+  int rc = guarded([&] {
+    if (!pivots || !centroid || !chunk_offsets || (!codes && num_pts > 0))
+      raise(GANN_ERR_INVALID, "NULL array");
+    if (num_pts < 0 || num_pts >= (int64_t(1) << 31)) raise(GANN_ERR_INVALID, "num_pts out of range");
+    check_chunks(chunk_offsets, dim, num_chunks);
+    int ndev = 0;
+    GANN_HIP(hipGetDeviceCount(&ndev));
+    if (device_id < 0 || device_id >= ndev) raise(GANN_ERR_INVALID, "device_id out of range");
+    GANN_HIP(hipSetDevice(device_id));
+    p = new gann_pq();
+    p->device = device_id;
+    GANN_HIP(hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking));
+    p->upload_static(pivots, centroid, chunk_offsets, dim, num_chunks);
+    if (codes_on_device) {
+      p->dev.codes = codes;
+      p->codes_borrowed = true;
+    } else {
+      upload(p->codes, codes, (size_t)num_pts * num_chunks);
+      p->dev.codes = p->codes.as<uint8_t>();
+    }
+    p->dev.num_pts = num_pts;
+  });
+  if (rc != GANN_OK) {
+    delete p;
+    return rc;
+  }
+  *out = p;
+  return GANN_OK;
+}
+
+int gann_pq_close(gann_pq* pq) {
+  if (!pq) return GANN_OK;
+  return guarded([&] {
+    GANN_HIP(hipSetDevice(pq->device));
+    delete pq;
+  });
+}
+
+int gann_handle_pq(gann_handle* h, gann_pq** out) {
+  if (!h || !out) {
+    g_err = "NULL argument";
+    return GANN_ERR_INVALID;
+  }
+  *out = &h->pq;
+  return GANN_OK;
+}
+
+int gann_pq_lut_build(gann_pq* pq, const float* q, int32_t nq, float* lut_out) {
+  return guarded([&] {
+    if (!pq) raise(GANN_ERR_INVALID, "pq is NULL");
+    if (nq < 0) raise(GANN_ERR_INVALID, "nq must be >= 0");
+    if (nq == 0) return;
+    if (!q || !lut_out) raise(GANN_ERR_INVALID, "NULL buffer");
+    GANN_HIP(hipSetDevice(pq->device));
+    hipStream_t s = pq->stream;
+    const size_t lut_bytes = (size_t)nq * pq->dev.M * gann::kNumPivots * 4;
+    pq->q.ensure((size_t)nq * pq->dev.dim * 4);
+    pq->out.ensure(lut_bytes);
+    GANN_HIP(hipMemcpyAsync(pq->q.p, q, (size_t)nq * pq->dev.dim * 4, hipMemcpyHostToDevice, s));
+    GANN_HIP(gann::launch_pq_lut(pq->dev, pq->q.as<float>(), nq, pq->out.as<float>(), s));
+    GANN_HIP(hipMemcpyAsync(lut_out, pq->out.p, lut_bytes, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipStreamSynchronize(s));
+  });
+}
+
+int gann_pq_adc_scan(gann_pq* pq, const float* q, int32_t nq, const int32_t* ids,
+                     int32_t ids_per_q, float* out) {
+  return guarded([&] {
+    if (!pq) raise(GANN_ERR_INVALID, "pq is NULL");
+    if (nq < 0 || ids_per_q < 0) raise(GANN_ERR_INVALID, "nq and ids_per_q must be >= 0");
+    if (nq == 0 || ids_per_q == 0) return;
+    if (!q || !ids || !out) raise(GANN_ERR_INVALID, "NULL buffer");
+    const int64_t n = (int64_t)nq * ids_per_q;
+    for (int64_t i = 0; i < n; ++i)
+      if (ids[i] < 0 || ids[i] >= pq->dev.num_pts)
+        raise(GANN_ERR_INVALID, "candidate id out of range at position " + std::to_string(i));
+    GANN_HIP(hipSetDevice(pq->device));
+    check_lds(gann::adc_smem_bytes(pq->dev.M, pq->dev.dim), pq->device, "ADC scan");
+    hipStream_t s = pq->stream;
+    pq->q.ensure((size_t)nq * pq->dev.dim * 4);
+    pq->ids.ensure((size_t)n * 4);
+    pq->out.ensure((size_t)n * 4);
+    GANN_HIP(hipMemcpyAsync(pq->q.p, q, (size_t)nq * pq->dev.dim * 4, hipMemcpyHostToDevice, s));
+    GANN_HIP(hipMemcpyAsync(pq->ids.p, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
+    GANN_HIP(gann::launch_pq_adc_scan(pq->dev, pq->q.as<float>(), nq, pq->ids.as<int32_t>(), ids_per_q,
+                                      pq->out.as<float>(), s));
+    GANN_HIP(hipMemcpyAsync(out, pq->out.p, (size_t)n * 4, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipStreamSynchronize(s));
+  });
+}
+
+int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const int32_t* ids_dev,
+                            int32_t ids_per_q, float* out_dev, void* stream) {
+  return guarded([&] {
+    if (!pq) raise(GANN_ERR_INVALID, "pq is NULL");
+    if (nq < 0 || ids_per_q < 0) raise(GANN_ERR_INVALID, "nq and ids_per_q must be >= 0");
+    if (nq == 0 || ids_per_q == 0) return;
+    if (!q_dev || !ids_dev || !out_dev) raise(GANN_ERR_INVALID, "NULL buffer");
+    GANN_HIP(hipSetDevice(pq->device));
+    check_lds(gann::adc_smem_bytes(pq->dev.M, pq->dev.dim), pq->device, "ADC scan");
+    hipStream_t s = stream ? (hipStream_t)stream : pq->stream;
+    GANN_HIP(gann::launch_pq_adc_scan(pq->dev, q_dev, nq, ids_dev, ids_per_q, out_dev, s));
+  });
+}
+
+}  // extern "C"

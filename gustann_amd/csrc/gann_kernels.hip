@@ -1,0 +1,684 @@
+// GustANN search kernels for MI355X (gfx950, wave64).
+//
+//  * pq_lut_kernel      : LUT build only (src/impl/pq.cuh:8-59), one
+//                         workgroup per query, LUT written to HBM.
+//  * pq_adc_scan_kernel : LUT build staged in LDS + ADC gather-scan over a
+//                         list of candidate ids per query
+//                         (src/impl/pure_mem.cuh:300-310 applied to an id list).
+//  * nav_entry_kernel   : pivot-graph entry selection (src/impl/nav.cuh:13-135)
+//                         with the map.txt translation (src/nav_graph.cu:104-109)
+//                         done on the device.
+//  * search_kernel      : the fused beam search of
+//                         src/impl/pure_mem.cuh:243-432, one wavefront per
+//                         query, LUT + candidate list + top-k in LDS.
+//  * step_round_kernel  : one expansion round of the step-wise form
+//                         (src/impl/hyd_search_v2.cuh:8-472) with the list in HBM.
+#include "gann_kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+
+#include "gann_device.hpp"
+
+namespace gann {
+
+// ------------------------------------------------------------------ LUT only
+
+__global__ __launch_bounds__(256) void pq_lut_kernel(PQDev pq, const float* __restrict__ q,
+                                                     int nq, float* __restrict__ lut_out) {
+  extern __shared__ float qs_smem[];
+  const int qi = blockIdx.x;
+  if (qi >= nq) return;
+  for (int i = threadIdx.x; i < pq.dim; i += blockDim.x)
+    qs_smem[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
+  __syncthreads();
+  lut_build(pq, qs_smem, lut_out + (int64_t)qi * pq.M * kPivots, threadIdx.x, blockDim.x);
+}
+
+// ------------------------------------------------------------------ ADC scan
+
+// One workgroup (256 lanes) per query.  LDS: LUT [M][256] f32 then q - mu.
+// Each lane scores ids tid, tid+256, ... in batches of kBatch rows whose
+// 16-byte code words are all requested before any LUT lookup, to keep many
+// independent HBM gathers in flight per lane.
+template <int MW, int kBatch>
+__global__ __launch_bounds__(256) void pq_adc_scan_kernel(PQDev pq, const float* __restrict__ q,
+                                                          int nq, const int32_t* __restrict__ ids,
+                                                          int S, float* __restrict__ out) {
+  extern __shared__ float smem[];
+  float* lut = smem;
+  float* qs = smem + pq.M * kPivots;
+  const int qi = blockIdx.x;
+  if (qi >= nq) return;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < pq.dim; i += blockDim.x)
+    qs[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
+  __syncthreads();
+  lut_build(pq, qs, lut, tid, blockDim.x);
+  __syncthreads();
+
+  const int32_t* qids = ids + (int64_t)qi * S;
+  float* qout = out + (int64_t)qi * S;
+  const int M = pq.M;
+  for (int s0 = 0; s0 < S; s0 += kBatch * (int)blockDim.x) {
+    int32_t id[kBatch];
+    CodeRow<MW> row[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      int s = s0 + b * (int)blockDim.x + tid;
+      const int32_t x = s < S ? __builtin_nontemporal_load(qids + s) : -1;
+      id[b] = (x >= 0 && (int64_t)x < pq.num_pts) ? x : -1;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+      if (id[b] >= 0) row[b].load(pq.codes + (int64_t)id[b] * M, M);
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      int s = s0 + b * (int)blockDim.x + tid;
+      if (s < S)
+        __builtin_nontemporal_store(
+            id[b] >= 0 ? row[b].adc(lut, pq.codes + (int64_t)id[b] * M, M) : __builtin_nanf(""),
+            qout + s);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ nav entry
+
+// One wavefront per query; lanes 0..31 hold the 32-slot pool of the
+// reference's warp (slot t in lane t), lanes 0..27 score the expanded node's
+// neighbours, each computing its full square_sum_32 value in-lane.
+template <typename T>
+__global__ __launch_bounds__(64) void nav_entry_kernel(NavDev nav, int64_t medoid, int64_t num_pts,
+                                                       int dim, const float* __restrict__ q,
+                                                       int nq, int32_t* __restrict__ entries,
+                                                       int32_t* __restrict__ local_out,
+                                                       int32_t* __restrict__ fallback_count) {
+  extern __shared__ float qv[];
+  const int qi = blockIdx.x;
+  if (qi >= nq) return;
+  const int lane = lane_id();
+  for (int i = lane; i < dim; i += kWave) qv[i] = q[(int64_t)qi * dim + i];
+  __syncthreads();
+  const T* data = reinterpret_cast<const T*>(nav.data);
+  constexpr int kKeep = 4, kExpand = 28;  // src/impl/nav.cuh:11-12
+  const int64_t total = nav.n * (int64_t)nav.max_m;
+
+  uint32_t pid = 0xffffffffu;
+  float pd = INFINITY;
+  {
+    float d0 = l2_square_sum_32<T>(qv, data + (int64_t)nav.start * dim, dim);
+    if (lane == 0) {
+      pid = (uint32_t)nav.start;
+      pd = d0;
+    }
+  }
+  int idx = 0;
+  const int64_t cap = 4 * nav.n + 64;
+  for (int64_t it = 0; idx != -1 && it < cap; ++it) {
+    const uint32_t u = (uint32_t)__shfl((int)pid, idx, kWave) & kMask31;
+    if (lane == idx) pid |= kVisited;
+    // neighbours: first <= 28 entries of the flat -1-padded array from u*max_m
+    const int64_t flat = (int64_t)u * nav.max_m + lane;
+    int32_t v = -1;
+    if (lane < kExpand && flat < total) v = nav.graph[flat];
+    const uint64_t stop = ballot64(lane >= kExpand || v == -1);
+    const int cnt = (int)__builtin_ctzll(stop);  // lanes < cnt hold neighbours
+    float dv = INFINITY;
+    if (lane < cnt) dv = l2_square_sum_32_inlane<T>(qv, data + (int64_t)v * dim, dim);
+    // neighbour t -> slot t + 4
+    const int src = lane - kKeep;
+    const int32_t v_sh = __shfl(v, src < 0 ? 0 : src, kWave);
+    const float d_sh = __shfl(dv, src < 0 ? 0 : src, kWave);
+    if (lane >= kKeep && lane < 32 && src < cnt) {
+      pid = (uint32_t)v_sh;
+      pd = d_sh;
+    }
+    // four selection steps (src/impl/nav.cuh:84-119)
+#pragma unroll
+    for (int i = 0; i < kKeep; ++i) {
+      float d = pd;
+      int pos = lane;
+      if (i != 0) {
+        const uint32_t prev = (uint32_t)__shfl((int)pid, i - 1, kWave);
+        const bool fold = lane < 32 && lane >= i && ((pid ^ prev) & kMask31) == 0;
+        const bool fold_vis = ballot64(fold && (pid & kVisited)) != 0;
+        if (fold) pd = INFINITY;
+        if (lane == i - 1 && fold_vis) pid |= kVisited;
+        d = fold ? INFINITY : pd;
+      }
+      if (lane < i) d = INFINITY;
+#pragma unroll
+      for (int off = 16; off > 0; off >>= 1) {
+        const float od = __shfl_down(d, off, 32);
+        const int op = __shfl_down(pos, off, 32);
+        if (od < d) {
+          d = od;
+          pos = op;
+        }
+      }
+      pos = __shfl(pos, 0, kWave);
+      if (i != pos) {
+        const float tv = __shfl(pd, i, kWave), yv = __shfl(pd, pos, kWave);
+        const uint32_t ti = (uint32_t)__shfl((int)pid, i, kWave);
+        const uint32_t yi = (uint32_t)__shfl((int)pid, pos, kWave);
+        if (tv != yv) {
+          if (lane == i) {
+            pd = yv;
+            pid = yi;
+          } else if (lane == pos) {
+            pd = tv;
+            pid = ti;
+          }
+        }
+      }
+    }
+    const uint64_t unv = ballot64(lane < 32 && !(pid & kVisited));
+    const int x = unv ? (int)__builtin_ctzll(unv) : 32;
+    idx = x < kKeep ? x : -1;
+  }
+  if (lane == 0) {
+    const int32_t local = (int32_t)(pid & kMask31);
+    int32_t base = -1;
+    if (local >= 0 && local < nav.n) base = nav.map[local];
+    if (base < 0 || base >= num_pts) {
+      base = (int32_t)medoid;
+      atomicAdd(fallback_count, 1);
+    }
+    entries[qi] = base;
+    if (local_out) local_out[qi] = local;
+  }
+}
+
+// ------------------------------------------------------------------ beam search
+
+// Per-expansion step shared by the fused and the step-wise kernels.
+// State in LDS: list A (sorted, distinct masked ids, visited bit in bit 31
+// of the low word), scratch B (merge target), N (sorted new run).
+// Returns the next node (or -1) and updates *sz.
+struct StepCtx {
+  uint64_t* A;
+  uint64_t* B;
+  uint64_t* N;
+  int L;
+};
+
+// Lower bound of `key` in a[0..n) compared by entry_key (first element whose
+// key is not below `key`).
+__device__ __forceinline__ int lower_bound_entries(const uint64_t* a, int n, uint64_t key) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (entry_key(a[mid]) < key)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// Merge the sorted new run N[0..deg) (held one per lane in `nkey`) into
+// A[0..sz) as src/impl/pure_mem.cuh:350-377 does, dedup + select as :380-419.
+// Returns the selected node id or -1; *sz is the new list size.
+__device__ __forceinline__ int32_t merge_dedup_select(const StepCtx& c, uint64_t nkey, int deg,
+                                                      int* sz_io) {
+  const int lane = lane_id();
+  const int sz = *sz_io;
+  const int L = c.L;
+  // new item rank: lower_bound in the old list, +1 if that slot holds the
+  // same id (the new copy goes right after the old one) (:351-361)
+  if (lane < deg) {
+    c.N[lane] = nkey;
+    int r = lower_bound_entries(c.A, sz, nkey);
+    if (r < sz && ((entry_id(c.A[r]) ^ (uint32_t)nkey) & kMask31) == 0) ++r;
+    c.B[r + lane] = nkey;
+  }
+  __syncthreads();
+  // old item rank: lower_bound in the new run (:363-369)
+  for (int i = lane; i < sz; i += kWave) {
+    const uint64_t e = c.A[i];
+    c.B[i + lower_bound_entries(c.N, deg, entry_key(e))] = e;
+  }
+  __syncthreads();
+  const int sz2 = min(sz + deg, 2 * L);  // (:377)
+  // dedup adjacent equal ids, compact into A, first unvisited (:380-419)
+  int count = 0;
+  int sel = -1;
+  for (int base = 0; base < sz2; base += kWave) {
+    const int i = base + lane;
+    const bool in = i < sz2;
+    uint64_t e = 0;
+    bool flag = false;
+    if (in) {
+      e = c.B[i];
+      if (i > 0) flag = ((entry_id(c.B[i - 1]) ^ entry_id(e)) & kMask31) == 0;
+    }
+    const uint64_t fmask = ballot64(in && flag);
+    const int mv = i - count - rank_below(fmask);
+    if (in && !flag) c.A[mv] = e;
+    const uint64_t cand = ballot64(in && !flag && !(entry_id(e) & kVisited));
+    if (sel < 0 && cand) {
+      const int first = (int)__builtin_ctzll(cand);
+      sel = __shfl(mv, first, kWave);
+    }
+    count += __popcll(fmask);
+  }
+  __syncthreads();
+  int32_t next = -1;
+  if (sel >= 0 && sel < L) {
+    const uint64_t e = c.A[sel];
+    next = (int32_t)(entry_id(e) & kMask31);
+    *sz_io = min(sz2 - count, L);
+    __syncthreads();
+    if (lane == 0) c.A[sel] = e | kVisited;
+  } else {
+    *sz_io = min(sz2 - count, L);
+  }
+  __syncthreads();
+  return next;
+}
+
+// Top-k insertion of (d, id) into the sorted LDS list (src/impl/util.cuh:116-163):
+// the value lands after the last element that is not greater than it,
+// greater elements shift right, the list keeps at most k.
+__device__ __forceinline__ void topk_push(float* td, int32_t* ti, int* found, int k, float d,
+                                          int32_t id) {
+  const int lane = lane_id();
+  const int n = *found;
+  // position = 1 + index of the last element with !(elem > d)
+  int pos = 0;
+  for (int base = 0; base < n; base += kWave) {
+    const int j = base + lane;
+    const uint64_t ng = ballot64(j < n && !(td[j] > d));
+    if (ng) pos = base + 64 - (int)__builtin_clzll(ng);
+  }
+  // shift [pos, last) right by one, last chunk first; the element at index
+  // k-1 of a full list falls off
+  const int last = min(n, k - 1);
+  if (last > pos) {
+    for (int base = ((last - 1) / kWave) * kWave; base >= (pos / kWave) * kWave; base -= kWave) {
+      const int j = base + lane;
+      const bool mv = j >= pos && j < last;
+      float vd = 0.f;
+      int32_t vi = 0;
+      if (mv) {
+        vd = td[j];
+        vi = ti[j];
+      }
+      __syncthreads();
+      if (mv) {
+        td[j + 1] = vd;
+        ti[j + 1] = vi;
+      }
+      __syncthreads();
+    }
+  }
+  if (lane == 0 && pos < k) {
+    td[pos] = d;
+    ti[pos] = id;
+  }
+  if (n + 1 <= k) *found = n + 1;
+  __syncthreads();
+}
+
+template <typename T>
+__device__ __forceinline__ const uint8_t* record_of(const IndexDev& ix, int64_t u) {
+  return ix.pages + (u / ix.nodes_per_page) * 4096 + (u % ix.nodes_per_page) * ix.node_len;
+}
+
+// LDS carve-up of the fused kernel (bytes): LUT | qr | A | B | N | topk dist | topk id
+struct SearchSmem {
+  static __host__ __device__ size_t bytes(int M, int dim, int L, int R, int k) {
+    size_t cap = (size_t)(L + R);
+    return (size_t)M * kPivots * 4 + (size_t)((dim + 1) & ~1) * 4 + cap * 8 * 2 + kWave * 8 +
+           (size_t)k * 8;
+  }
+};
+
+template <typename T, int MW>
+__global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
+                                                    const float* __restrict__ q, int nq,
+                                                    const int32_t* __restrict__ entries, int topk,
+                                                    int L, int32_t* __restrict__ nns,
+                                                    float* __restrict__ dists,
+                                                    int32_t* __restrict__ found_cnt,
+                                                    int32_t* __restrict__ n_exp,
+                                                    int32_t* __restrict__ n_adc) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  const int qi = blockIdx.x;
+  if (qi >= nq) return;
+  const int lane = lane_id();
+  const int dim = ix.dim, M = pq.M, R = ix.R;
+  float* lut = reinterpret_cast<float*>(smem_raw);
+  float* qr = lut + M * kPivots;
+  uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
+  uint64_t* B = A + (L + R);
+  uint64_t* N = B + (L + R);
+  float* td = reinterpret_cast<float*>(N + kWave);
+  int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
+
+  // q - mu into qr for the LUT build, then the restored query
+  // fl(fl(q - mu) + mu) that the reference's rerank reads (src/impl/pq.cuh:22-24, 54-56)
+  const float* qq = q + (int64_t)qi * dim;
+  for (int i = lane; i < dim; i += kWave) qr[i] = qq[i] - pq.centroid[i];
+  __syncthreads();
+  lut_build(pq, qr, lut, lane, kWave);
+  __syncthreads();
+  for (int i = lane; i < dim; i += kWave) qr[i] = qr[i] + pq.centroid[i];
+  __syncthreads();
+
+  StepCtx c{A, B, N, L};
+  int sz = 0;
+  int found = 0;
+  int32_t u = entries[qi];
+  int32_t exps = 0, adcs = 0;
+  const int64_t cap = ix.num_pts + 2;
+  while (u >= 0 && exps < cap) {
+    ++exps;
+    const uint8_t* rec = record_of<T>(ix, u);
+    int deg = *reinterpret_cast<const int32_t*>(rec + ix.data_len);
+    deg = __builtin_amdgcn_readfirstlane(min(max(deg, 0), R));
+    adcs += deg;
+    const uint32_t* edge = reinterpret_cast<const uint32_t*>(rec + ix.data_len + 4);
+    uint32_t v = 0;
+    uint64_t key = ~(uint64_t)0;  // padding sorts last
+    if (lane < deg) {
+      v = edge[lane];
+      CodeRow<MW> row;
+      const uint8_t* crow = pq.codes + (int64_t)v * M;
+      row.load(crow, M);
+      key = make_key(row.adc(lut, crow, M), v);
+    }
+    // exact rerank of u (independent of the list update; :420-423)
+    const float du = l2_square_sum_32<T>(qr, reinterpret_cast<const T*>(rec), dim);
+    key = wave_sort64(key);
+    const int32_t next = merge_dedup_select(c, key, deg, &sz);
+    topk_push(td, ti, &found, topk, du, u);
+    u = __builtin_amdgcn_readfirstlane(next);
+  }
+  // results; slots past found stay 0 as in the reference's zero-initialised vectors
+  for (int j = lane; j < topk; j += kWave) {
+    const bool ok = j < found;
+    nns[(int64_t)qi * topk + j] = ok ? ti[j] : 0;
+    dists[(int64_t)qi * topk + j] = ok ? td[j] : 0.0f;
+  }
+  if (lane == 0) {
+    found_cnt[qi] = found;
+    if (n_exp) n_exp[qi] = exps;
+    if (n_adc) n_adc[qi] = adcs;
+  }
+}
+
+// ------------------------------------------------------------------ step-wise
+
+// Per-query state of the step-wise form, kept in HBM between rounds
+// (the role of Data{visited_cnt,size} + request[] in src/impl/hyd.cuh:6-9,
+// src/impl/hyd_search_v2.cuh:35, :450-458).
+struct StepState {
+  int32_t u;      // node to expand this round, -1 when done
+  int32_t sz;     // list size
+  int32_t found;  // top-k fill
+  int32_t exps;   // expansions so far
+  int32_t adcs;   // ADC evaluations so far
+};
+
+// Builds each query's LUT into HBM (the role of init_search,
+// src/hyd_task_runner.cu:12-15) and initialises its state.
+__global__ __launch_bounds__(64) void step_init_kernel(PQDev pq, const float* __restrict__ q,
+                                                       int nq, const int32_t* __restrict__ entries,
+                                                       float* __restrict__ luts,
+                                                       StepState* __restrict__ st) {
+  extern __shared__ float qs[];
+  const int qi = blockIdx.x;
+  if (qi >= nq) return;
+  const int lane = lane_id();
+  for (int i = lane; i < pq.dim; i += kWave) qs[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
+  __syncthreads();
+  lut_build(pq, qs, luts + (int64_t)qi * pq.M * kPivots, lane, kWave);
+  if (lane == 0) st[qi] = StepState{entries[qi], 0, 0, 0, 0};
+}
+
+// One expansion per active query: the work of merge_data_kernel followed by
+// unify_kernel (src/impl/hyd_search_v2.cuh:8-351, 353-472) in one launch;
+// the candidate list and the top-k travel through HBM between rounds.
+template <typename T, int MW>
+__global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
+                                                        const float* __restrict__ q, int nq,
+                                                        const float* __restrict__ luts, int topk,
+                                                        int L, uint64_t* __restrict__ lists,
+                                                        StepState* __restrict__ st,
+                                                        int32_t* __restrict__ nns,
+                                                        float* __restrict__ dists,
+                                                        int32_t* __restrict__ active) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  const int qi = blockIdx.x;
+  if (qi >= nq) return;
+  StepState s = st[qi];
+  if (s.u < 0) return;
+  const int lane = lane_id();
+  const int dim = ix.dim, M = pq.M, R = ix.R;
+  const int cap = L + R;
+  float* qr = reinterpret_cast<float*>(smem_raw);
+  uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
+  uint64_t* B = A + cap;
+  uint64_t* N = B + cap;
+  float* td = reinterpret_cast<float*>(N + kWave);
+  int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
+  const float* lut = luts + (int64_t)qi * M * kPivots;
+  uint64_t* glist = lists + (int64_t)qi * cap;
+
+  const float* qq = q + (int64_t)qi * dim;
+  for (int i = lane; i < dim; i += kWave) {
+    float t = qq[i] - pq.centroid[i];
+    qr[i] = t + pq.centroid[i];
+  }
+  for (int i = lane; i < s.sz; i += kWave) A[i] = glist[i];
+  for (int j = lane; j < s.found; j += kWave) {
+    td[j] = dists[(int64_t)qi * topk + j];
+    ti[j] = nns[(int64_t)qi * topk + j];
+  }
+  __syncthreads();
+
+  const int32_t u = s.u;
+  const uint8_t* rec = record_of<T>(ix, u);
+  int deg = *reinterpret_cast<const int32_t*>(rec + ix.data_len);
+  deg = __builtin_amdgcn_readfirstlane(min(max(deg, 0), R));
+  const uint32_t* edge = reinterpret_cast<const uint32_t*>(rec + ix.data_len + 4);
+  uint64_t key = ~(uint64_t)0;
+  if (lane < deg) {
+    const uint32_t v = edge[lane];
+    CodeRow<MW> row;
+    const uint8_t* crow = pq.codes + (int64_t)v * M;
+    row.load(crow, M);
+    key = make_key(row.adc(lut, crow, M), v);
+  }
+  const float du = l2_square_sum_32<T>(qr, reinterpret_cast<const T*>(rec), dim);
+  key = wave_sort64(key);
+  StepCtx c{A, B, N, L};
+  int sz = s.sz;
+  const int32_t next = merge_dedup_select(c, key, deg, &sz);
+  int found = s.found;
+  topk_push(td, ti, &found, topk, du, u);
+
+  for (int i = lane; i < sz; i += kWave) glist[i] = A[i];
+  for (int j = lane; j < found; j += kWave) {
+    dists[(int64_t)qi * topk + j] = td[j];
+    nns[(int64_t)qi * topk + j] = ti[j];
+  }
+  if (lane == 0) {
+    const int32_t exps = s.exps + 1;
+    const bool done = next < 0 || exps >= ix.num_pts + 2;
+    st[qi] = StepState{done ? -1 : next, sz, found, exps, s.adcs + deg};
+    if (done) atomicSub(active, 1);
+  }
+}
+
+// Finalises the step-wise results: zero the unfilled slots, counts out.
+__global__ void step_finish_kernel(int nq, int topk, const StepState* __restrict__ st,
+                                   int32_t* __restrict__ nns, float* __restrict__ dists,
+                                   int32_t* __restrict__ found_cnt, int32_t* __restrict__ n_exp,
+                                   int32_t* __restrict__ n_adc) {
+  const int qi = blockIdx.x;
+  if (qi >= nq) return;
+  const StepState s = st[qi];
+  for (int j = threadIdx.x; j < topk; j += blockDim.x) {
+    if (j >= s.found) {
+      nns[(int64_t)qi * topk + j] = 0;
+      dists[(int64_t)qi * topk + j] = 0.0f;
+    }
+  }
+  if (threadIdx.x == 0) {
+    found_cnt[qi] = s.found;
+    if (n_exp) n_exp[qi] = s.exps;
+    if (n_adc) n_adc[qi] = s.adcs;
+  }
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// ------------------------------------------------------------------ launchers
+
+namespace {
+template <int MW>
+hipError_t launch_adc(const PQDev& pq, const float* q, int nq, const int32_t* ids, int S,
+                      float* out, hipStream_t stream) {
+  size_t smem = (size_t)pq.M * kPivots * 4 + (size_t)pq.dim * 4;
+  constexpr int kBatch = MW == 0 ? 4 : (MW <= 2 ? 8 : 4);
+  hipLaunchKernelGGL((pq_adc_scan_kernel<MW, kBatch>), dim3(nq), dim3(256), smem, stream, pq, q, nq,
+                     ids, S, out);
+  return hipGetLastError();
+}
+
+template <typename T, int MW>
+hipError_t launch_search_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
+                           const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
+                           int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream) {
+  size_t smem = SearchSmem::bytes(pq.M, ix.dim, L, ix.R, topk);
+  hipLaunchKernelGGL((search_kernel<T, MW>), dim3(nq), dim3(64), smem, stream, ix, pq, q, nq,
+                     entries, topk, L, nns, dists, found, n_exp, n_adc);
+  return hipGetLastError();
+}
+
+template <typename T, int MW>
+hipError_t launch_round_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
+                          const float* luts, int topk, int L, uint64_t* lists, StepState* st,
+                          int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
+  size_t cap = (size_t)(L + ix.R);
+  size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + cap * 16 + kWave * 8 + (size_t)topk * 8;
+  hipLaunchKernelGGL((step_round_kernel<T, MW>), dim3(nq), dim3(64), smem, stream, ix, pq, q, nq,
+                     luts, topk, L, lists, st, nns, dists, active);
+  return hipGetLastError();
+}
+
+int mw_of(int M) {
+  if (M % 16 != 0) return 0;
+  int mw = M / 16;
+  return (mw >= 1 && mw <= 4) ? mw : 0;
+}
+}  // namespace
+
+size_t search_smem_bytes(int M, int dim, int L, int R, int topk) {
+  return SearchSmem::bytes(M, dim, L, R, topk);
+}
+
+size_t adc_smem_bytes(int M, int dim) { return (size_t)M * kPivots * 4 + (size_t)dim * 4; }
+
+hipError_t launch_pq_lut(const PQDev& pq, const float* q, int nq, float* lut_out,
+                         hipStream_t stream) {
+  hipLaunchKernelGGL(pq_lut_kernel, dim3(nq), dim3(256), (size_t)pq.dim * 4, stream, pq, q, nq,
+                     lut_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_pq_adc_scan(const PQDev& pq, const float* q, int nq, const int32_t* ids, int S,
+                              float* out, hipStream_t stream) {
+  switch (mw_of(pq.M)) {
+    case 1: return launch_adc<1>(pq, q, nq, ids, S, out, stream);
+    case 2: return launch_adc<2>(pq, q, nq, ids, S, out, stream);
+    case 3: return launch_adc<3>(pq, q, nq, ids, S, out, stream);
+    case 4: return launch_adc<4>(pq, q, nq, ids, S, out, stream);
+    default: return launch_adc<0>(pq, q, nq, ids, S, out, stream);
+  }
+}
+
+hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_t num_pts, int dim,
+                            const float* q, int nq, int32_t* entries, int32_t* local_out,
+                            int32_t* fallback_count, hipStream_t stream) {
+  size_t smem = (size_t)dim * 4;
+  if (dtype == 0)
+    hipLaunchKernelGGL(nav_entry_kernel<uint8_t>, dim3(nq), dim3(64), smem, stream, nav, medoid,
+                       num_pts, dim, q, nq, entries, local_out, fallback_count);
+  else
+    hipLaunchKernelGGL(nav_entry_kernel<float>, dim3(nq), dim3(64), smem, stream, nav, medoid,
+                       num_pts, dim, q, nq, entries, local_out, fallback_count);
+  return hipGetLastError();
+}
+
+hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                         const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
+                         int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream) {
+  const int mw = mw_of(pq.M);
+#define GANN_SEARCH_CASE(T)                                                                        \
+  switch (mw) {                                                                                    \
+    case 1: return launch_search_t<T, 1>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
+    case 2: return launch_search_t<T, 2>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
+    case 3: return launch_search_t<T, 3>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
+    case 4: return launch_search_t<T, 4>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
+    default: return launch_search_t<T, 0>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
+  }
+  if (dtype == 0) {
+    GANN_SEARCH_CASE(uint8_t)
+  } else {
+    GANN_SEARCH_CASE(float)
+  }
+#undef GANN_SEARCH_CASE
+}
+
+size_t step_state_bytes() { return sizeof(StepState); }
+
+hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
+                            float* luts, void* st, hipStream_t stream) {
+  hipLaunchKernelGGL(step_init_kernel, dim3(nq), dim3(64), (size_t)pq.dim * 4, stream, pq, q, nq,
+                     entries, luts, reinterpret_cast<StepState*>(st));
+  return hipGetLastError();
+}
+
+hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                             const float* luts, int topk, int L, uint64_t* lists, void* st,
+                             int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
+  StepState* s = reinterpret_cast<StepState*>(st);
+  const int mw = mw_of(pq.M);
+#define GANN_ROUND_CASE(T)                                                                        \
+  switch (mw) {                                                                                   \
+    case 1: return launch_round_t<T, 1>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
+    case 2: return launch_round_t<T, 2>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
+    case 3: return launch_round_t<T, 3>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
+    case 4: return launch_round_t<T, 4>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
+    default: return launch_round_t<T, 0>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
+  }
+  if (dtype == 0) {
+    GANN_ROUND_CASE(uint8_t)
+  } else {
+    GANN_ROUND_CASE(float)
+  }
+#undef GANN_ROUND_CASE
+}
+
+hipError_t launch_step_finish(int nq, int topk, const void* st, int32_t* nns, float* dists,
+                              int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream) {
+  hipLaunchKernelGGL(step_finish_kernel, dim3(nq), dim3(64), 0, stream, nq, topk,
+                     reinterpret_cast<const StepState*>(st), nns, dists, found, n_exp, n_adc);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, n, v);
+  return hipGetLastError();
+}
+
+}  // namespace gann

@@ -1,0 +1,35 @@
+// Host-side launchers of the GustANN HIP kernels (defined in gann_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gann_device.hpp"
+
+namespace gann {
+
+size_t search_smem_bytes(int M, int dim, int L, int R, int topk);
+size_t adc_smem_bytes(int M, int dim);
+size_t step_state_bytes();
+
+hipError_t launch_pq_lut(const PQDev& pq, const float* q, int nq, float* lut_out,
+                         hipStream_t stream);
+hipError_t launch_pq_adc_scan(const PQDev& pq, const float* q, int nq, const int32_t* ids, int S,
+                              float* out, hipStream_t stream);
+hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_t num_pts, int dim,
+                            const float* q, int nq, int32_t* entries, int32_t* local_out,
+                            int32_t* fallback_count, hipStream_t stream);
+hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                         const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
+                         int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
+hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
+                            float* luts, void* st, hipStream_t stream);
+hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                             const float* luts, int topk, int L, uint64_t* lists, void* st,
+                             int32_t* nns, float* dists, int32_t* active, hipStream_t stream);
+hipError_t launch_step_finish(int nq, int topk, const void* st, int32_t* nns, float* dists,
+                              int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
+
+}  // namespace gann

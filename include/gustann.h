@@ -1,0 +1,150 @@
+/* gustann.h — C ABI of libgustann_hip.so, the MI355X (gfx950) implementation
+ * of GustANN's in-GPU search path.
+ *
+ * Every entry point returns an int status (GANN_OK == 0); on failure
+ * gann_last_error() describes the cause (thread-local).  No C++ exception
+ * crosses this boundary.  Handles are not thread-safe: one thread per handle,
+ * or external locking.  Each handle owns one HIP stream on its device.
+ *
+ * Reference interfaces replaced (1799364931/GustANN):
+ *   GustANN::GustANN(DataType)                 src/ssd_search.hpp:70
+ *   GustANN::init_pure_mem(cfg, use_gpu_mem)   src/ssd_search.hpp:76, src/ssd_search.cu:108-112
+ *   GustANN::search(q, nq, topk, L, nns, dists, found_cnt, stats)
+ *                                              src/ssd_search.hpp:78-80, src/pure_mem.cu:71-199
+ *   GustANN::~GustANN()                        src/ssd_search.cu:28-53
+ *   PQSearch::read_data / init_device          src/pq_search.cu:56-185
+ *   PQSearchData::init_query (LUT build)       src/impl/pq.cuh:8-59
+ *   ADC scan                                   src/impl/pure_mem.cuh:300-310
+ *   get_entry_kernel + NavGraph::translate     src/impl/nav.cuh:13-147, src/nav_graph.cu:104-109
+ */
+#ifndef GUSTANN_H
+#define GUSTANN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes */
+#define GANN_OK 0
+#define GANN_ERR_INVALID 1     /* bad argument (the reference asserted or threw) */
+#define GANN_ERR_IO 2          /* file missing / unreadable (the reference called exit(-1)) */
+#define GANN_ERR_FORMAT 3      /* malformed index file */
+#define GANN_ERR_HIP 4         /* HIP runtime failure (the reference's CHECK_CUDA threw) */
+#define GANN_ERR_NOMEM 5       /* device or pinned host allocation failed */
+#define GANN_ERR_UNSUPPORTED 6 /* valid request outside what this build implements */
+
+/* ---- enums */
+#define GANN_UINT8 0 /* DataType UINT8, src/common.hpp:22-25 */
+#define GANN_FLOAT 1 /* DataType FLOAT */
+
+#define GANN_PLACEMENT_HBM 0         /* search_mem -G: index pages copied to HBM */
+#define GANN_PLACEMENT_HOST_PINNED 1 /* search_mem without -G: pages read zero-copy from pinned host memory */
+
+#define GANN_MODE_FUSED 0    /* one persistent kernel per search (src/impl/pure_mem.cuh:243-432) */
+#define GANN_MODE_STEPWISE 1 /* one launch per expansion round, list in HBM (src/impl/hyd_search_v2.cuh) */
+
+typedef struct gann_handle gann_handle;
+typedef struct gann_pq gann_pq;
+
+/* GustANNConfig (src/ssd_search.hpp:18-23) plus the data type, placement and
+ * device that the reference took from its constructor, -G flag and
+ * CUDA_VISIBLE_DEVICES. */
+typedef struct gann_config {
+  const char* index_file; /* <prefix>_disk.index */
+  const char* pq_prefix;  /* <pq>_pivots.bin, <pq>_compressed.bin (required) */
+  const char* nav_prefix; /* directory with nav_index, nav_index.data, map.txt; NULL or "" = none */
+  int32_t dtype;          /* GANN_UINT8 / GANN_FLOAT */
+  int32_t placement;      /* GANN_PLACEMENT_* */
+  int32_t device_id;
+} gann_config;
+
+/* GustANNStats (src/ssd_search.hpp:25-27) extended with device counters. */
+typedef struct gann_stats {
+  double run_time_s;      /* wall clock of entry selection + search, the scope of src/pure_mem.cu:101-187 */
+  double entry_time_s;    /* wall clock of entry selection alone */
+  int64_t n_expansions;   /* node expansions summed over queries */
+  int64_t n_adc;          /* ADC evaluations summed over queries */
+  double alg_bytes;       /* algorithmic bytes: per expansion record + deg*M codes, per query q + results */
+  int64_t n_nav_fallback; /* queries whose pivot entry fell outside map.txt (entry = medoid) */
+} gann_stats;
+
+typedef struct gann_index_info {
+  int64_t num_pts, dim, medoid, max_m, node_len, nodes_per_page, num_pages;
+  int32_t dtype, num_chunks;
+  int64_t nav_num_node;
+  int32_t nav_max_m, nav_start;
+} gann_index_info;
+
+const char* gann_last_error(void);
+const char* gann_version(void);
+
+/* ---- index handle (GustANN facade, PURE_MEM executor) */
+
+/* GustANN(dtype) + init_pure_mem(cfg, placement == HBM). Loads the disk
+ * index, the PQ tables and the optional pivot graph, validates every node
+ * record (deg <= R, neighbour ids < num_pts, no repeated id in a list) and
+ * makes the index resident on the device. */
+int gann_open(const gann_config* cfg, gann_handle** out);
+int gann_close(gann_handle* h);
+int gann_get_info(const gann_handle* h, gann_index_info* info);
+
+/* GustANN::search.  Synchronous; q is [nq][dim] f32 row-major on the host;
+ * nns/dists are [nq][topk], found_cnt [nq] on the host.  Requires
+ * L >= topk (bin/search_disk.cpp:189-192).  beam_width must be 1, the
+ * reference's one node per iteration.  st may be NULL. */
+int gann_search(gann_handle* h, const float* q, int32_t nq, int32_t topk, int32_t L,
+                int32_t beam_width, int32_t* nns, float* dists, int32_t* found_cnt,
+                gann_stats* st);
+
+/* gann_search with an explicit execution mode (GANN_MODE_*); n_exp (nullable,
+ * [nq]) receives each query's expansion count. */
+int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int32_t L,
+                   int32_t beam_width, int32_t mode, int32_t* nns, float* dists,
+                   int32_t* found_cnt, int32_t* n_exp, gann_stats* st);
+
+/* Asynchronous fused search on device buffers already resident in HBM,
+ * enqueued on `stream` (a hipStream_t; NULL = the handle's stream).
+ * entries_dev: [nq] device scratch for the entry ids.  n_exp_dev/n_adc_dev
+ * nullable [nq]. */
+int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                       int32_t* entries_dev, int32_t* nns_dev, float* dists_dev,
+                       int32_t* found_dev, int32_t* n_exp_dev, int32_t* n_adc_dev, void* stream);
+
+/* get_entry_kernel + NavGraph::translate: base-graph entry per query (the
+ * medoid when the handle has no pivot graph).  local_out (nullable) receives
+ * the pivot-local ids. */
+int gann_nav_entry(gann_handle* h, const float* q, int32_t nq, int32_t* entries_out,
+                   int32_t* local_out);
+
+/* ---- PQ tables */
+
+/* PQSearch::read_data + init_device for a standalone PQ (no graph). */
+int gann_pq_open(const char* pq_prefix, int32_t device_id, gann_pq** out);
+/* PQ from arrays: pivots [256][dim], centroid [dim], chunk_offsets [M+1]
+ * (0 .. dim, non-decreasing), codes [num_pts][M].  codes_on_device != 0
+ * borrows a device pointer (the caller keeps it alive); otherwise the codes
+ * are copied to HBM. */
+int gann_pq_create(const float* pivots, const float* centroid, const int32_t* chunk_offsets,
+                   int32_t dim, int32_t num_chunks, const uint8_t* codes, int64_t num_pts,
+                   int32_t codes_on_device, int32_t device_id, gann_pq** out);
+int gann_pq_close(gann_pq* pq);
+/* The PQ tables of an open handle (borrowed; valid until gann_close). */
+int gann_handle_pq(gann_handle* h, gann_pq** out);
+
+/* LUT build (src/impl/pq.cuh:8-59): lut_out [nq][M][256] on the host. */
+int gann_pq_lut_build(gann_pq* pq, const float* q, int32_t nq, float* lut_out);
+/* LUT + ADC gather-scan: out[i][s] = ADC(LUT(q_i), codes[ids[i][s]]); ids
+ * [nq][ids_per_q] on the host, each in [0, num_pts). */
+int gann_pq_adc_scan(gann_pq* pq, const float* q, int32_t nq, const int32_t* ids,
+                     int32_t ids_per_q, float* out);
+/* Asynchronous LUT + ADC gather-scan on device buffers, enqueued on `stream`
+ * (a hipStream_t; NULL = the PQ's stream).  Ids outside [0, num_pts) give NaN. */
+int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const int32_t* ids_dev,
+                            int32_t ids_per_q, float* out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GUSTANN_H */
