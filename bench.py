@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Benchmark of the GustANN MI355X search path.
+
+Default workload (the PQ kernel microbenchmark): 10,000 f32 queries of dim
+128, PQ with M = 32 subspaces x 256 centroids, 100,000,000 random 32-byte code
+rows resident in HBM, 4096 uniformly random candidate ids per query.  One
+step = one launch of the fused LUT-build + ADC gather-scan kernel over all
+queries.  Prints one JSON line:
+
+  value      queries/s of the kernel (inputs already resident in HBM)
+  roofline   algorithmic bytes per launch / average launch time vs 8 TB/s
+  cpu_baseline  the CPU oracle on a bounded sample of the same workload
+
+``--workload search`` runs the in-memory beam search on a synthetic
+uint8 mixture index instead (built on the fly; slower to set up).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "QPS @ recall@10=0.9 on 1 MI355X; ADC-scan HBM GB/s vs peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def adc_alg_bytes(nq, dim, S, M):
+    """Algorithmic bytes of one ADC launch: per query the query vector (4*dim),
+    per candidate its code row (M), its id (4) and its distance (4); once the
+    static pivots, centroid and chunk map."""
+    return nq * (4 * dim + S * (M + 8)) + (256 * dim * 4 + 4 * dim + 4 * dim)
+
+
+def cpu_baseline_adc(pq_np, codes_host, Q, ids_host, target_s):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    threads = min(16, os.cpu_count() or 1)
+    piv, cen, off = pq_np
+    # calibrate on a small batch, then run about target_s of work: a prefix
+    # of the queries, or whole passes over all of them when one pass is short
+    n0 = min(64, Q.shape[0])
+    t = time.perf_counter()
+    orc.adc_scan(piv, cen, off, codes_host, Q[:n0], ids_host[:n0], threads)
+    per_q = (time.perf_counter() - t) / n0
+    n = int(min(Q.shape[0], max(n0, target_s / max(per_q, 1e-9))))
+    passes = max(1, int(target_s / max(per_q * n, 1e-9))) if n == Q.shape[0] else 1
+    t = time.perf_counter()
+    for _ in range(passes):
+        out = orc.adc_scan(piv, cen, off, codes_host, Q[:n], ids_host[:n], threads)
+    dt = time.perf_counter() - t
+    return {"value": passes * n / dt, "unit": "queries/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} pass(es) over the first {n} of the {Q.shape[0]} queries x "
+                      f"{ids_host.shape[1]} ids: oracle/gann_oracle.c orc_adc_scan over the full "
+                      f"host copy of the codes, {threads} threads, {dt:.1f} s"}, out
+
+
+def traffic_from_profiles(name):
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def bench_adc(args):
+    import torch
+    from gustann_amd.search import PQSearch
+
+    nq, dim, M, S, N = args.nq, 128, 32, args.ids_per_query, args.num_codes
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(2024)
+    Q = rng.uniform(0, 255, size=(nq, dim)).astype(np.float32)
+    piv = rng.uniform(-16, 16, size=(256, dim)).astype(np.float32)
+    cen = rng.uniform(96, 160, size=dim).astype(np.float32)
+    off = np.arange(0, dim + 1, dim // M, dtype=np.int32)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    log(f"[bench] generating {N} x {M} codes and {nq} x {S} ids on the device")
+    codes = torch.randint(0, 256, (N, M), dtype=torch.uint8, device=dev, generator=g)
+    ids = torch.randint(0, N, (nq, S), dtype=torch.int32, device=dev, generator=g)
+    q_dev = torch.from_numpy(Q).to(dev)
+    out = torch.empty((nq, S), dtype=torch.float32, device=dev)
+    pq = PQSearch.create(piv, cen, off, codes_device_ptr=codes.data_ptr(), num_pts=N)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    def step():
+        pq.adc_scan_device(q_dev.data_ptr(), nq, ids.data_ptr(), S, out.data_ptr(), sp)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    value = nq / (ms / 1e3)
+    alg = adc_alg_bytes(nq, dim, S, M)
+    achieved = alg / (ms / 1e3) / 1e9
+    log(f"[bench] {args.steps} steps: {ms:.4f} ms/step (events), wall {wall:.3f} s, "
+        f"{achieved:.1f} GB/s algorithmic")
+
+    result = {
+        "metric": METRIC, "value": value, "unit": "queries/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (uniform random codes, ids and queries, seeded)",
+        "config": {"workload": "pq_adc_microbench", "nq": nq, "dim": dim, "M": M, "K": 256,
+                   "num_codes": N, "ids_per_query": S},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic_from_profiles("adc_scan_c1_traffic.json"),
+                     "alg_bytes_per_launch": alg},
+    }
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle) on a bounded sample")
+        codes_host = codes.cpu().numpy()
+        ids_host = ids.cpu().numpy()
+        cpu, cpu_out = cpu_baseline_adc((piv, cen, off), codes_host, Q, ids_host, args.cpu_seconds)
+        result["cpu_baseline"] = cpu
+        gpu_out = out[: cpu_out.shape[0]].cpu().numpy()
+        result["parity_sample_bitexact"] = bool(np.array_equal(gpu_out.view(np.uint32),
+                                                               cpu_out.view(np.uint32)))
+    pq.close()
+    return result
+
+
+def bench_search(args):
+    import torch
+    from gustann_amd import index as gi
+    from gustann_amd.search import GustANN, GustANNConfig, UINT8
+
+    spec = gi.DatasetSpec(name=f"mix{args.n}", n=args.n, dim=128, nclusters=args.nclusters, R=64,
+                          L_build=100, M=32, nq=args.nq_search, k=10, nav_n=args.nav_n)
+    out_dir = args.data_dir or os.path.join("/tmp", f"gann_{spec.name}_{args.nav_n}")
+    meta_path = os.path.join(out_dir, "meta.json")
+    if os.path.exists(meta_path):
+        meta = json.load(open(meta_path))
+    else:
+        log(f"[bench] building {spec.name} under {out_dir}")
+        meta = gi.build_dataset(spec, out_dir, verbose=True)
+    P = meta["paths"]
+    Q = gi.read_vecs(P["query"], np.uint8).astype(np.float32)
+    gt = gi.read_vecs(P["gt"], np.int32)
+    g = GustANN(UINT8)
+    g.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), True)
+    dev = torch.device("cuda:0")
+    rep = args.repeat
+    Qr = np.tile(Q, (rep, 1))
+    nq = Qr.shape[0]
+    q_dev = torch.from_numpy(Qr).to(dev)
+    ent = torch.empty(nq, dtype=torch.int32, device=dev)
+    nns = torch.empty((nq, 10), dtype=torch.int32, device=dev)
+    dd = torch.empty((nq, 10), dtype=torch.float32, device=dev)
+    fc = torch.empty(nq, dtype=torch.int32, device=dev)
+    ne = torch.empty(nq, dtype=torch.int32, device=dev)
+    na = torch.empty(nq, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    rows = []
+    for L in args.L:
+        def step():
+            g.search_device(q_dev.data_ptr(), nq, 10, L, ent.data_ptr(), nns.data_ptr(), dd.data_ptr(),
+                            fc.data_ptr(), ne.data_ptr(), na.data_ptr(), stream.cuda_stream)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        res = nns[: Q.shape[0]].cpu().numpy()
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        rec = orc.recall(res, gt[:, :10], 10)
+        exps = int(ne.sum().item())
+        adcs = int(na.sum().item())
+        alg = exps * (128 + 4) + adcs * (4 + 32) + nq * (4 * 128 + 80)
+        rows.append({"L": L, "ms": ms, "qps": nq / (ms / 1e3), "recall": rec,
+                     "expansions_per_query": exps / nq, "alg_GBps": alg / (ms / 1e3) / 1e9})
+        log(f"[bench] L={L} {ms:.3f} ms qps={nq / (ms / 1e3):.0f} recall@10={rec:.4f}")
+    best = next((r for r in rows if r["recall"] >= 0.9), rows[-1])
+    g.close()
+    return {
+        "metric": METRIC, "value": best["qps"], "unit": "queries/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": best["ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8/f32",
+        "data": "synthetic uint8 Gaussian mixture",
+        "config": {"workload": f"in_memory_search_{args.n}x128_u8", "nq": nq, "L_sweep": rows},
+        "roofline": {"bound": "hbm", "achieved": best["alg_GBps"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": best["alg_GBps"] / HBM_PEAK_GBS, "traffic": None},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=["adc", "search"], default="adc")
+    ap.add_argument("--nq", type=int, default=10000)
+    ap.add_argument("--ids-per-query", type=int, default=4096)
+    ap.add_argument("--num-codes", type=int, default=100_000_000)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--n", type=int, default=1_000_000)
+    ap.add_argument("--nclusters", type=int, default=1000)
+    ap.add_argument("--nav-n", type=int, default=0)
+    ap.add_argument("--nq-search", type=int, default=10000)
+    ap.add_argument("--repeat", type=int, default=1)
+    ap.add_argument("--L", type=int, nargs="+", default=[32, 48, 64, 96, 128])
+    ap.add_argument("--data-dir", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU (queries shard across "
+                                   "GPUs with no collective, so one GPU's figure is the unit); "
+                                   "--gpus must be 1"}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    res = bench_adc(args) if args.workload == "adc" else bench_search(args)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -80,6 +80,23 @@ def lib_path(name: str) -> str:
     return os.path.join(_LIB_DIR, name)
 
 
+def _preload_torch_hip_runtime():
+    """PyTorch-ROCm wheels ship their own libamdhip64 with the same SONAME
+    (libamdhip64.so.7) as /opt/rocm's.  Loading ours first would bring a second
+    HIP runtime into the process once torch is imported, and the second one
+    finds no device.  When torch is installed, load its runtime first so that
+    libgustann_hip.so binds to it by SONAME and the process has one runtime."""
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return
+    for loc in spec.submodule_search_locations:
+        cand = os.path.join(loc, "lib", "libamdhip64.so")
+        if os.path.exists(cand):
+            C.CDLL(cand, mode=C.RTLD_GLOBAL)
+            return
+
+
 def hip_lib():
     """libgustann_hip.so, loaded once.  Raises if it has not been built."""
     global _hip
@@ -88,6 +105,7 @@ def hip_lib():
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is missing: run `python -m gustann_amd.build` first "
                                "(the search path has no CPU fallback)")
+        _preload_torch_hip_runtime()
         lib = C.CDLL(path)
         for name, (res, args) in _SIGS.items():
             fn = getattr(lib, name)
@@ -119,6 +137,7 @@ _IDX_SIGS = {
     "gib_write_pq": (C.c_int, [C.c_char_p, _P, _P, _P, _I32, _I32, _P, _I64]),
     "gib_write_nav": (C.c_int, [C.c_char_p, _P, _I64, _I64, _I64, _P, _P, _I64, _I32, _P]),
     "gib_write_vecs": (C.c_int, [C.c_char_p, _I64, _I64, _I64, _P]),
+    "gib_inspect": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p, _I64, _P]),
 }
 
 

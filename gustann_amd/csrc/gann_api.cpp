@@ -184,6 +184,11 @@ struct gann_pq {
     upload(chunk_off, off, (size_t)(M + 1) * 4);
     dev.dim = dim;
     dev.M = M;
+    // uniform chunks [m*w, (m+1)*w) select the unrolled LUT build
+    int w = dim % M == 0 ? dim / M : 0;
+    for (int m = 0; m <= M && w; ++m)
+      if (off[m] != m * w) w = 0;
+    dev.chunk_w = w;
     dev.pivots_t = pivots_t.as<float>();
     dev.centroid = centroid.as<float>();
     dev.chunk_off = chunk_off.as<int32_t>();
@@ -552,7 +557,7 @@ int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t t
     if (!q_dev || !entries_dev || !nns_dev || !dists_dev || !found_dev)
       raise(GANN_ERR_INVALID, "NULL buffer");
     GANN_HIP(hipSetDevice(h->device));
-    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    hipStream_t s = (hipStream_t)stream;
     h->counters.ensure(64);
     run_entries(h, q_dev, nq, entries_dev, nullptr, h->counters.as<int32_t>(), s);
     run_search(h, q_dev, nq, topk, L, GANN_MODE_FUSED, entries_dev, nns_dev, dists_dev, found_dev,
@@ -730,7 +735,7 @@ int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const i
     if (!q_dev || !ids_dev || !out_dev) raise(GANN_ERR_INVALID, "NULL buffer");
     GANN_HIP(hipSetDevice(pq->device));
     check_lds(gann::adc_smem_bytes(pq->dev.M, pq->dev.dim), pq->device, "ADC scan");
-    hipStream_t s = stream ? (hipStream_t)stream : pq->stream;
+    hipStream_t s = (hipStream_t)stream;
     GANN_HIP(gann::launch_pq_adc_scan(pq->dev, q_dev, nq, ids_dev, ids_per_q, out_dev, s));
   });
 }

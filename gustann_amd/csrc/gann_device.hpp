@@ -19,6 +19,7 @@ constexpr uint32_t kVisited = 0x80000000u;
 struct PQDev {
   int32_t dim;
   int32_t M;
+  int32_t chunk_w;          // > 0: chunk m spans dims [m*chunk_w, (m+1)*chunk_w); 0: irregular
   int64_t num_pts;
   const float* pivots_t;    // [dim][256]  (transposed like src/pq_search.cu:88-93)
   const float* centroid;    // [dim]
@@ -148,19 +149,72 @@ __device__ __forceinline__ float l2_square_sum_32_inlane(const float* q, const T
 // Builds the LUT of one query into `lut` ([M][256], LDS or global) with the
 // reference's arithmetic (src/impl/pq.cuh:8-59): row m accumulates
 // (q_i - mu_i - P[k][i])^2 over its dims in ascending order from 0.
-// qs must already hold q - centroid.  Work is split over `nthreads` threads
-// starting at `tid`, one pivot column per thread.
+// qs must already hold q - centroid.
+//
+// Thread layout: lane (tid & 63) owns the pivot quad 4*lane .. 4*lane+3 and
+// reads it as one float4 of pivots_t[i][*]; the (nthreads / 64) wave groups
+// split the chunks.  W > 0: every chunk spans W consecutive dims (the
+// compile-time common case, fully unrolled so all pivot loads of a chunk
+// group are in flight together); W == 0: chunk bounds from chunk_off.
+template <int W>
 __device__ __forceinline__ void lut_build(const PQDev& pq, const float* qs, float* lut, int tid,
                                           int nthreads) {
-  for (int j = tid; j < kPivots; j += nthreads) {
-    for (int m = 0; m < pq.M; ++m) {
-      float acc = 0.0f;
+  const int quad = tid & 63;
+  const int group = tid >> 6, ngroups = nthreads >> 6;
+  const float4* pt = reinterpret_cast<const float4*>(pq.pivots_t);
+  float4* lut4 = reinterpret_cast<float4*>(lut);
+  if constexpr (W > 0) {
+    constexpr int kU = W >= 4 ? 2 : (W == 1 ? 8 : 4);  // chunks per batch
+    int m = group;
+    for (; m + (kU - 1) * ngroups < pq.M; m += kU * ngroups) {
+      float4 p[kU][W];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int w = 0; w < W; ++w) p[u][w] = pt[(int64_t)((m + u * ngroups) * W + w) * 64 + quad];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float q = qs[(m + u * ngroups) * W + w];
+          float d;
+          d = q - p[u][w].x; acc.x = fma_f(d, d, acc.x);
+          d = q - p[u][w].y; acc.y = fma_f(d, d, acc.y);
+          d = q - p[u][w].z; acc.z = fma_f(d, d, acc.z);
+          d = q - p[u][w].w; acc.w = fma_f(d, d, acc.w);
+        }
+        lut4[(m + u * ngroups) * 64 + quad] = acc;
+      }
+    }
+    for (; m < pq.M; m += ngroups) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float4 pv = pt[(int64_t)(m * W + w) * 64 + quad];
+        const float q = qs[m * W + w];
+        float d;
+        d = q - pv.x; acc.x = fma_f(d, d, acc.x);
+        d = q - pv.y; acc.y = fma_f(d, d, acc.y);
+        d = q - pv.z; acc.z = fma_f(d, d, acc.z);
+        d = q - pv.w; acc.w = fma_f(d, d, acc.w);
+      }
+      lut4[m * 64 + quad] = acc;
+    }
+  } else {
+    for (int m = group; m < pq.M; m += ngroups) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
       const int lo = pq.chunk_off[m], hi = pq.chunk_off[m + 1];
       for (int i = lo; i < hi; ++i) {
-        float d = qs[i] - pq.pivots_t[(int64_t)i * kPivots + j];
-        acc = fma_f(d, d, acc);
+        const float4 pv = pt[(int64_t)i * 64 + quad];
+        const float q = qs[i];
+        float d;
+        d = q - pv.x; acc.x = fma_f(d, d, acc.x);
+        d = q - pv.y; acc.y = fma_f(d, d, acc.y);
+        d = q - pv.z; acc.z = fma_f(d, d, acc.z);
+        d = q - pv.w; acc.w = fma_f(d, d, acc.w);
       }
-      lut[m * kPivots + j] = acc;
+      lut4[m * 64 + quad] = acc;
     }
   }
 }
@@ -177,7 +231,7 @@ struct CodeRow {
     if constexpr (MW > 0) {
       const u32x4* p = reinterpret_cast<const u32x4*>(row);
 #pragma unroll
-      for (int k = 0; k < MW; ++k) w[k] = __builtin_nontemporal_load(p + k);
+      for (int k = 0; k < MW; ++k) w[k] = p[k];
     } else {
       (void)row;
       (void)M;

@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <type_traits>
 
 #include "gann_device.hpp"
 
@@ -25,6 +26,7 @@ namespace gann {
 
 // ------------------------------------------------------------------ LUT only
 
+template <int W>
 __global__ __launch_bounds__(256) void pq_lut_kernel(PQDev pq, const float* __restrict__ q,
                                                      int nq, float* __restrict__ lut_out) {
   extern __shared__ float qs_smem[];
@@ -33,16 +35,19 @@ __global__ __launch_bounds__(256) void pq_lut_kernel(PQDev pq, const float* __re
   for (int i = threadIdx.x; i < pq.dim; i += blockDim.x)
     qs_smem[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
   __syncthreads();
-  lut_build(pq, qs_smem, lut_out + (int64_t)qi * pq.M * kPivots, threadIdx.x, blockDim.x);
+  lut_build<W>(pq, qs_smem, lut_out + (int64_t)qi * pq.M * kPivots, threadIdx.x, blockDim.x);
 }
 
 // ------------------------------------------------------------------ ADC scan
 
 // One workgroup (256 lanes) per query.  LDS: LUT [M][256] f32 then q - mu.
-// Each lane scores ids tid, tid+256, ... in batches of kBatch rows whose
-// 16-byte code words are all requested before any LUT lookup, to keep many
-// independent HBM gathers in flight per lane.
-template <int MW, int kBatch>
+// Each lane scores ids tid, tid+256, ... in batches of kBatch rows.  The
+// first batch of ids and code rows is requested before the LUT is built, and
+// each following batch right after the previous one is summed, so the random
+// row gathers (the bound of this kernel) overlap the LUT build and the LDS
+// lookups.  Code rows use ordinary cached loads: on gfx950 nontemporal loads
+// cut the random-row request rate by about a fifth.
+template <int MW, int W, int kBatch>
 __global__ __launch_bounds__(256) void pq_adc_scan_kernel(PQDev pq, const float* __restrict__ q,
                                                           int nq, const int32_t* __restrict__ ids,
                                                           int S, float* __restrict__ out) {
@@ -52,34 +57,41 @@ __global__ __launch_bounds__(256) void pq_adc_scan_kernel(PQDev pq, const float*
   const int qi = blockIdx.x;
   if (qi >= nq) return;
   const int tid = threadIdx.x;
-  for (int i = tid; i < pq.dim; i += blockDim.x)
-    qs[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
-  __syncthreads();
-  lut_build(pq, qs, lut, tid, blockDim.x);
-  __syncthreads();
-
+  const int nt = blockDim.x;
+  const int M = pq.M;
   const int32_t* qids = ids + (int64_t)qi * S;
   float* qout = out + (int64_t)qi * S;
-  const int M = pq.M;
-  for (int s0 = 0; s0 < S; s0 += kBatch * (int)blockDim.x) {
-    int32_t id[kBatch];
-    CodeRow<MW> row[kBatch];
+
+  int32_t id[kBatch];
+  CodeRow<MW> row[kBatch];
+  auto request = [&](int s0) {
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
-      int s = s0 + b * (int)blockDim.x + tid;
-      const int32_t x = s < S ? __builtin_nontemporal_load(qids + s) : -1;
+      const int s = s0 + b * nt + tid;
+      const int32_t x = s < S ? qids[s] : -1;
       id[b] = (x >= 0 && (int64_t)x < pq.num_pts) ? x : -1;
     }
 #pragma unroll
     for (int b = 0; b < kBatch; ++b)
       if (id[b] >= 0) row[b].load(pq.codes + (int64_t)id[b] * M, M);
+  };
+  request(0);
+
+  for (int i = tid; i < pq.dim; i += nt) qs[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
+  __syncthreads();
+  lut_build<W>(pq, qs, lut, tid, nt);
+  __syncthreads();
+
+  for (int s0 = 0; s0 < S; s0 += kBatch * nt) {
+    float d[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+      d[b] = id[b] >= 0 ? row[b].adc(lut, pq.codes + (int64_t)id[b] * M, M) : __builtin_nanf("");
+    if (s0 + kBatch * nt < S) request(s0 + kBatch * nt);
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
-      int s = s0 + b * (int)blockDim.x + tid;
-      if (s < S)
-        __builtin_nontemporal_store(
-            id[b] >= 0 ? row[b].adc(lut, pq.codes + (int64_t)id[b] * M, M) : __builtin_nanf(""),
-            qout + s);
+      const int s = s0 + b * nt + tid;
+      if (s < S) __builtin_nontemporal_store(d[b], qout + s);
     }
   }
 }
@@ -336,7 +348,7 @@ struct SearchSmem {
   }
 };
 
-template <typename T, int MW>
+template <typename T, int MW, int W>
 __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
                                                     const float* __restrict__ q, int nq,
                                                     const int32_t* __restrict__ entries, int topk,
@@ -363,7 +375,7 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   const float* qq = q + (int64_t)qi * dim;
   for (int i = lane; i < dim; i += kWave) qr[i] = qq[i] - pq.centroid[i];
   __syncthreads();
-  lut_build(pq, qr, lut, lane, kWave);
+  lut_build<W>(pq, qr, lut, lane, kWave);
   __syncthreads();
   for (int i = lane; i < dim; i += kWave) qr[i] = qr[i] + pq.centroid[i];
   __syncthreads();
@@ -425,6 +437,7 @@ struct StepState {
 
 // Builds each query's LUT into HBM (the role of init_search,
 // src/hyd_task_runner.cu:12-15) and initialises its state.
+template <int W>
 __global__ __launch_bounds__(64) void step_init_kernel(PQDev pq, const float* __restrict__ q,
                                                        int nq, const int32_t* __restrict__ entries,
                                                        float* __restrict__ luts,
@@ -435,7 +448,7 @@ __global__ __launch_bounds__(64) void step_init_kernel(PQDev pq, const float* __
   const int lane = lane_id();
   for (int i = lane; i < pq.dim; i += kWave) qs[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
   __syncthreads();
-  lut_build(pq, qs, luts + (int64_t)qi * pq.M * kPivots, lane, kWave);
+  lut_build<W>(pq, qs, luts + (int64_t)qi * pq.M * kPivots, lane, kWave);
   if (lane == 0) st[qi] = StepState{entries[qi], 0, 0, 0, 0};
 }
 
@@ -543,41 +556,32 @@ __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
 // ------------------------------------------------------------------ launchers
 
 namespace {
-template <int MW>
-hipError_t launch_adc(const PQDev& pq, const float* q, int nq, const int32_t* ids, int S,
-                      float* out, hipStream_t stream) {
-  size_t smem = (size_t)pq.M * kPivots * 4 + (size_t)pq.dim * 4;
-  constexpr int kBatch = MW == 0 ? 4 : (MW <= 2 ? 8 : 4);
-  hipLaunchKernelGGL((pq_adc_scan_kernel<MW, kBatch>), dim3(nq), dim3(256), smem, stream, pq, q, nq,
-                     ids, S, out);
-  return hipGetLastError();
-}
-
-template <typename T, int MW>
-hipError_t launch_search_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
-                           const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
-                           int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream) {
-  size_t smem = SearchSmem::bytes(pq.M, ix.dim, L, ix.R, topk);
-  hipLaunchKernelGGL((search_kernel<T, MW>), dim3(nq), dim3(64), smem, stream, ix, pq, q, nq,
-                     entries, topk, L, nns, dists, found, n_exp, n_adc);
-  return hipGetLastError();
-}
-
-template <typename T, int MW>
-hipError_t launch_round_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
-                          const float* luts, int topk, int L, uint64_t* lists, StepState* st,
-                          int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
-  size_t cap = (size_t)(L + ix.R);
-  size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + cap * 16 + kWave * 8 + (size_t)topk * 8;
-  hipLaunchKernelGGL((step_round_kernel<T, MW>), dim3(nq), dim3(64), smem, stream, ix, pq, q, nq,
-                     luts, topk, L, lists, st, nns, dists, active);
-  return hipGetLastError();
-}
-
 int mw_of(int M) {
   if (M % 16 != 0) return 0;
-  int mw = M / 16;
+  const int mw = M / 16;
   return (mw >= 1 && mw <= 4) ? mw : 0;
+}
+int w_of(int chunk_w) { return (chunk_w == 2 || chunk_w == 4) ? chunk_w : 0; }
+
+// Calls f(std::integral_constant<int, MW>{}) for the runtime code-row shape.
+template <class F>
+hipError_t with_mw(int M, F&& f) {
+  switch (mw_of(M)) {
+    case 1: return f(std::integral_constant<int, 1>{});
+    case 2: return f(std::integral_constant<int, 2>{});
+    case 3: return f(std::integral_constant<int, 3>{});
+    case 4: return f(std::integral_constant<int, 4>{});
+    default: return f(std::integral_constant<int, 0>{});
+  }
+}
+// Calls f(std::integral_constant<int, W>{}) for the runtime chunk width.
+template <class F>
+hipError_t with_w(int chunk_w, F&& f) {
+  switch (w_of(chunk_w)) {
+    case 2: return f(std::integral_constant<int, 2>{});
+    case 4: return f(std::integral_constant<int, 4>{});
+    default: return f(std::integral_constant<int, 0>{});
+  }
 }
 }  // namespace
 
@@ -589,20 +593,25 @@ size_t adc_smem_bytes(int M, int dim) { return (size_t)M * kPivots * 4 + (size_t
 
 hipError_t launch_pq_lut(const PQDev& pq, const float* q, int nq, float* lut_out,
                          hipStream_t stream) {
-  hipLaunchKernelGGL(pq_lut_kernel, dim3(nq), dim3(256), (size_t)pq.dim * 4, stream, pq, q, nq,
-                     lut_out);
-  return hipGetLastError();
+  return with_w(pq.chunk_w, [&](auto w) {
+    hipLaunchKernelGGL((pq_lut_kernel<decltype(w)::value>), dim3(nq), dim3(256),
+                       (size_t)pq.dim * 4, stream, pq, q, nq, lut_out);
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_pq_adc_scan(const PQDev& pq, const float* q, int nq, const int32_t* ids, int S,
                               float* out, hipStream_t stream) {
-  switch (mw_of(pq.M)) {
-    case 1: return launch_adc<1>(pq, q, nq, ids, S, out, stream);
-    case 2: return launch_adc<2>(pq, q, nq, ids, S, out, stream);
-    case 3: return launch_adc<3>(pq, q, nq, ids, S, out, stream);
-    case 4: return launch_adc<4>(pq, q, nq, ids, S, out, stream);
-    default: return launch_adc<0>(pq, q, nq, ids, S, out, stream);
-  }
+  const size_t smem = adc_smem_bytes(pq.M, pq.dim);
+  return with_mw(pq.M, [&](auto mw) {
+    return with_w(pq.chunk_w, [&](auto w) {
+      constexpr int MW = decltype(mw)::value;
+      constexpr int kBatch = MW == 0 ? 4 : (MW <= 2 ? 8 : 4);
+      hipLaunchKernelGGL((pq_adc_scan_kernel<MW, decltype(w)::value, kBatch>), dim3(nq), dim3(256),
+                         smem, stream, pq, q, nq, ids, S, out);
+      return hipGetLastError();
+    });
+  });
 }
 
 hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_t num_pts, int dim,
@@ -618,54 +627,66 @@ hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_
   return hipGetLastError();
 }
 
+namespace {
+template <typename T>
+hipError_t launch_search_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
+                           const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
+                           int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream) {
+  const size_t smem = SearchSmem::bytes(pq.M, ix.dim, L, ix.R, topk);
+  return with_mw(pq.M, [&](auto mw) {
+    return with_w(pq.chunk_w, [&](auto w) {
+      hipLaunchKernelGGL((search_kernel<T, decltype(mw)::value, decltype(w)::value>), dim3(nq),
+                         dim3(64), smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found,
+                         n_exp, n_adc);
+      return hipGetLastError();
+    });
+  });
+}
+
+template <typename T>
+hipError_t launch_round_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
+                          const float* luts, int topk, int L, uint64_t* lists, StepState* st,
+                          int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
+  const size_t cap = (size_t)(L + ix.R);
+  const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + cap * 16 + kWave * 8 + (size_t)topk * 8;
+  return with_mw(pq.M, [&](auto mw) {
+    hipLaunchKernelGGL((step_round_kernel<T, decltype(mw)::value>), dim3(nq), dim3(64), smem,
+                       stream, ix, pq, q, nq, luts, topk, L, lists, st, nns, dists, active);
+    return hipGetLastError();
+  });
+}
+}  // namespace
+
 hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                          const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                          int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream) {
-  const int mw = mw_of(pq.M);
-#define GANN_SEARCH_CASE(T)                                                                        \
-  switch (mw) {                                                                                    \
-    case 1: return launch_search_t<T, 1>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
-    case 2: return launch_search_t<T, 2>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
-    case 3: return launch_search_t<T, 3>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
-    case 4: return launch_search_t<T, 4>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
-    default: return launch_search_t<T, 0>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, stream); \
-  }
-  if (dtype == 0) {
-    GANN_SEARCH_CASE(uint8_t)
-  } else {
-    GANN_SEARCH_CASE(float)
-  }
-#undef GANN_SEARCH_CASE
+  if (dtype == 0)
+    return launch_search_t<uint8_t>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp,
+                                    n_adc, stream);
+  return launch_search_t<float>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
+                                stream);
 }
 
 size_t step_state_bytes() { return sizeof(StepState); }
 
 hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
                             float* luts, void* st, hipStream_t stream) {
-  hipLaunchKernelGGL(step_init_kernel, dim3(nq), dim3(64), (size_t)pq.dim * 4, stream, pq, q, nq,
-                     entries, luts, reinterpret_cast<StepState*>(st));
-  return hipGetLastError();
+  return with_w(pq.chunk_w, [&](auto w) {
+    hipLaunchKernelGGL((step_init_kernel<decltype(w)::value>), dim3(nq), dim3(64),
+                       (size_t)pq.dim * 4, stream, pq, q, nq, entries, luts,
+                       reinterpret_cast<StepState*>(st));
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                              const float* luts, int topk, int L, uint64_t* lists, void* st,
                              int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
   StepState* s = reinterpret_cast<StepState*>(st);
-  const int mw = mw_of(pq.M);
-#define GANN_ROUND_CASE(T)                                                                        \
-  switch (mw) {                                                                                   \
-    case 1: return launch_round_t<T, 1>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
-    case 2: return launch_round_t<T, 2>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
-    case 3: return launch_round_t<T, 3>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
-    case 4: return launch_round_t<T, 4>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
-    default: return launch_round_t<T, 0>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream); \
-  }
-  if (dtype == 0) {
-    GANN_ROUND_CASE(uint8_t)
-  } else {
-    GANN_ROUND_CASE(float)
-  }
-#undef GANN_ROUND_CASE
+  if (dtype == 0)
+    return launch_round_t<uint8_t>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active,
+                                   stream);
+  return launch_round_t<float>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream);
 }
 
 hipError_t launch_step_finish(int nq, int topk, const void* st, int32_t* nns, float* dists,
@@ -677,7 +698,8 @@ hipError_t launch_step_finish(int nq, int topk, const void* st, int32_t* nns, fl
 
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, n, v);
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
+                     n, v);
   return hipGetLastError();
 }
 

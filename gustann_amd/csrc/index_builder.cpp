@@ -672,6 +672,25 @@ int gib_write_nav(const char* dir, const void* data, int64_t n, int64_t dim, int
   return 0;
 }
 
+// Parses an index with the same readers libgustann_hip.so uses (formats.hpp),
+// without a device: out[0..11] = num_pts, dim, medoid, node_len,
+// nodes_per_page, max_m, num_pages, pq_dim, pq_num_chunks, pq_num_pts,
+// nav_num_node, nav_max_m.  nav_prefix may be NULL or "".
+int gib_inspect(const char* index_file, const char* pq_prefix, const char* nav_prefix,
+                int64_t elem_size, int64_t* out) {
+  gann::DiskLayout L;
+  if (!gann::parse_disk_meta(index_file, elem_size, &L, &g_err)) return 1;
+  gann::PQHost pq;
+  std::string pp(pq_prefix);
+  if (!gann::read_pq(pp + "_pivots.bin", pp + "_compressed.bin", &pq, true, &g_err)) return 1;
+  gann::NavHost nav;
+  if (nav_prefix && *nav_prefix && !gann::read_nav(nav_prefix, elem_size, &nav, &g_err)) return 1;
+  int64_t v[12] = {L.num_pts, L.dim, L.medoid, L.node_len, L.nodes_per_page, L.max_m, L.num_pages,
+                   pq.dim, pq.num_chunks, pq.num_pts, nav.num_node, nav.max_m};
+  std::memcpy(out, v, sizeof(v));
+  return 0;
+}
+
 int gib_write_vecs(const char* path, int64_t elem, int64_t n, int64_t d, const void* data) {
   if (!gann::write_vecs(path, (size_t)elem, n, d, data, &g_err)) return 1;
   return 0;

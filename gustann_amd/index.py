@@ -157,6 +157,18 @@ def write_vecs(path, A):
                                       _ptr(A)))
 
 
+def inspect(index_file, pq_prefix, nav_prefix="", elem_size=1):
+    """Parses an index with the C++ readers of the search library; returns a
+    dict of its layout or raises RuntimeError with the reader's message."""
+    out = np.zeros(12, np.int64)
+    icheck(index_lib().gib_inspect(os.fsencode(index_file), os.fsencode(pq_prefix),
+                                   os.fsencode(nav_prefix) if nav_prefix else None, elem_size,
+                                   _ptr(out)))
+    keys = ("num_pts", "dim", "medoid", "node_len", "nodes_per_page", "max_m", "num_pages",
+            "pq_dim", "pq_num_chunks", "pq_num_pts", "nav_num_node", "nav_max_m")
+    return dict(zip(keys, (int(v) for v in out)))
+
+
 def read_pq(prefix):
     """<pq>_pivots.bin + <pq>_compressed.bin (src/pq_search.cu:56-121) as a
     PQTables (legacy nr = 5 offset tables read chunk offsets from slot 3)."""

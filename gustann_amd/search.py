@@ -81,7 +81,7 @@ class GustANN:
                mode: int = N.MODE_FUSED, n_exp=None):
         """GustANN::search (src/ssd_search.cu:114-140).  qdata: [nq][dim] f32.
         Output arrays are filled in place when given; all are returned."""
-        q = _f32(qdata).reshape(num_queries, -1)
+        q = _f32(qdata).reshape(num_queries, int(self.info.dim) if self.info else -1)
         if nns is None:
             nns = np.empty((num_queries, topk), np.int32)
         if distances is None:
@@ -193,7 +193,9 @@ class PQSearch:
 
     def adc_scan(self, q, ids) -> np.ndarray:
         q = _f32(q).reshape(-1, self.dim)
-        ids = np.ascontiguousarray(ids, np.int32).reshape(q.shape[0], -1)
+        ids = np.ascontiguousarray(ids, np.int32)
+        if ids.ndim != 2 or ids.shape[0] != q.shape[0]:
+            raise ValueError("ids must be [nq][ids_per_q]")
         out = np.empty(ids.shape, np.float32)
         N.check(N.hip_lib().gann_pq_adc_scan(self._p, q.ctypes.data, q.shape[0], ids.ctypes.data,
                                              ids.shape[1], out.ctypes.data))

@@ -105,7 +105,7 @@ int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int
                    int32_t* found_cnt, int32_t* n_exp, gann_stats* st);
 
 /* Asynchronous fused search on device buffers already resident in HBM,
- * enqueued on `stream` (a hipStream_t; NULL = the handle's stream).
+ * enqueued on `stream` (a hipStream_t; 0 = the default stream).
  * entries_dev: [nq] device scratch for the entry ids.  n_exp_dev/n_adc_dev
  * nullable [nq]. */
 int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
@@ -140,7 +140,7 @@ int gann_pq_lut_build(gann_pq* pq, const float* q, int32_t nq, float* lut_out);
 int gann_pq_adc_scan(gann_pq* pq, const float* q, int32_t nq, const int32_t* ids,
                      int32_t ids_per_q, float* out);
 /* Asynchronous LUT + ADC gather-scan on device buffers, enqueued on `stream`
- * (a hipStream_t; NULL = the PQ's stream).  Ids outside [0, num_pts) give NaN. */
+ * (a hipStream_t; 0 = the default stream).  Ids outside [0, num_pts) give NaN. */
 int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const int32_t* ids_dev,
                             int32_t ids_per_q, float* out_dev, void* stream);
 
