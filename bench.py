@@ -65,6 +65,16 @@ def cpu_baseline_adc(pq_np, codes_host, Q, ids_host, target_s):
                       f"host copy of the codes, {threads} threads, {dt:.1f} s"}, out
 
 
+def recall_at_k(res, gt, k):
+    """calc_recall (bin/utils.hpp:104-116): hits of each result slot in the set
+    of the first k ground-truth ids, over the ground-truth rows."""
+    hits = 0
+    for r, g in zip(res, gt):
+        s = set(int(x) for x in g[:k])
+        hits += sum(1 for x in r[:k] if int(x) in s)
+    return hits / (gt.shape[0] * k)
+
+
 def traffic_from_profiles(name):
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
@@ -151,7 +161,8 @@ def bench_search(args):
     from gustann_amd.search import GustANN, GustANNConfig, UINT8
 
     spec = gi.DatasetSpec(name=f"mix{args.n}", n=args.n, dim=128, nclusters=args.nclusters, R=64,
-                          L_build=100, M=32, nq=args.nq_search, k=10, nav_n=args.nav_n)
+                          L_build=100, M=32, nq=args.nq_search, k=10, nav_n=args.nav_n,
+                          gt_nq=args.gt_nq)
     out_dir = args.data_dir or os.path.join("/tmp", f"gann_{spec.name}_{args.nav_n}")
     meta_path = os.path.join(out_dir, "meta.json")
     if os.path.exists(meta_path):
@@ -191,10 +202,8 @@ def bench_search(args):
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / args.steps
-        res = nns[: Q.shape[0]].cpu().numpy()
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import oracle as orc
-        rec = orc.recall(res, gt[:, :10], 10)
+        res = nns[: gt.shape[0]].cpu().numpy()
+        rec = recall_at_k(res, gt, 10)
         exps = int(ne.sum().item())
         adcs = int(na.sum().item())
         alg = exps * (128 + 4) + adcs * (4 + 32) + nq * (4 * 128 + 80)
@@ -203,15 +212,63 @@ def bench_search(args):
         log(f"[bench] L={L} {ms:.3f} ms qps={nq / (ms / 1e3):.0f} recall@10={rec:.4f}")
     best = next((r for r in rows if r["recall"] >= 0.9), rows[-1])
     g.close()
-    return {
+    result = {
         "metric": METRIC, "value": best["qps"], "unit": "queries/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": best["ms"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8/f32",
         "data": "synthetic uint8 Gaussian mixture",
-        "config": {"workload": f"in_memory_search_{args.n}x128_u8", "nq": nq, "L_sweep": rows},
+        "config": {"workload": f"in_memory_search_{args.n}x128_u8", "nq": nq, "L": best["L"],
+                   "L_sweep": rows},
         "roofline": {"bound": "hbm", "achieved": best["alg_GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": best["alg_GBps"] / HBM_PEAK_GBS, "traffic": None},
     }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        log(f"[bench] CPU baseline (oracle beam search) at L={best['L']}")
+        ix = orc.Index(P["index"], P["pq"], P["nav"])
+        threads = min(16, os.cpu_count() or 1)
+        n0 = min(256, Q.shape[0])
+        t = time.perf_counter()
+        ix.search(Q[:n0], 10, best["L"], threads=threads)
+        per_q = (time.perf_counter() - t) / n0
+        n = int(min(Q.shape[0], max(n0, args.cpu_seconds / max(per_q, 1e-9))))
+        t = time.perf_counter()
+        on, od, of, _, _ = ix.search(Q[:n], 10, best["L"], threads=threads)
+        dt = time.perf_counter() - t
+        result["cpu_baseline"] = {"value": n / dt, "unit": "queries/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"first {n} queries at L={best['L']}: oracle/gann_oracle.c "
+                                            f"orc_search, {threads} threads, {dt:.1f} s"}
+        g2 = GustANN(UINT8)
+        g2.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), True)
+        gn, gd, gf = g2.search(Q[:n], n, 10, best["L"])
+        g2.close()
+        result["parity_sample_bitexact"] = bool(np.array_equal(gn, on) and np.array_equal(gf, of)
+                                                and np.array_equal(gd.view(np.uint32), od.view(np.uint32)))
+    return result
+
+
+def bench_copy(args):
+    """Calibration kernel for the HBM traffic counters: one device-to-device
+    copy of a buffer of known size (reads and writes copy_bytes each)."""
+    import torch
+    n = args.copy_bytes
+    dev = torch.device("cuda:0")
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    return {"workload": "copy", "copy_bytes": n, "ms_per_copy": ms,
+            "GBps_read_plus_write": 2 * n / (ms / 1e3) / 1e9}
 
 
 def main():
@@ -219,7 +276,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["adc", "search"], default="adc")
+    ap.add_argument("--workload", choices=["adc", "search", "copy"], default="adc")
+    ap.add_argument("--copy-bytes", type=int, default=1 << 31)
     ap.add_argument("--nq", type=int, default=10000)
     ap.add_argument("--ids-per-query", type=int, default=4096)
     ap.add_argument("--num-codes", type=int, default=100_000_000)
@@ -229,6 +287,7 @@ def main():
     ap.add_argument("--nclusters", type=int, default=1000)
     ap.add_argument("--nav-n", type=int, default=0)
     ap.add_argument("--nq-search", type=int, default=10000)
+    ap.add_argument("--gt-nq", type=int, default=1000)
     ap.add_argument("--repeat", type=int, default=1)
     ap.add_argument("--L", type=int, nargs="+", default=[32, 48, 64, 96, 128])
     ap.add_argument("--data-dir", default="")
@@ -242,7 +301,10 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
-    res = bench_adc(args) if args.workload == "adc" else bench_search(args)
+    if args.workload == "copy":
+        res = bench_copy(args)
+    else:
+        res = bench_adc(args) if args.workload == "adc" else bench_search(args)
     print(json.dumps(res), flush=True)
 
 

@@ -270,6 +270,11 @@ void open_handle(const gann_config* cfg, gann_handle* h) {
   if (!gann::parse_disk_meta(cfg->index_file, es, &h->layout, &err))
     raise(err.rfind("cannot open", 0) == 0 ? GANN_ERR_IO : GANN_ERR_FORMAT, err);
   const gann::DiskLayout& L = h->layout;
+  // The degree and neighbour ids follow the coordinates in each record and
+  // are read as 32-bit words (src/impl/pure_mem.cuh:290-292), which needs a
+  // 4-byte aligned coordinate block.
+  if (L.data_len % 4 != 0)
+    raise(GANN_ERR_UNSUPPORTED, "coordinate bytes per record must be a multiple of 4");
 
   // PQ (src/ssd_search.cu:59-67, src/pq_search.cu:56-121)
   {
@@ -371,6 +376,8 @@ void validate_search(const gann_handle* h, int32_t nq, int32_t topk, int32_t L, 
   if (beam != 1) raise(GANN_ERR_UNSUPPORTED, "beam_width must be 1 (one node per iteration)");
   if (h->layout.max_m > 64)
     raise(GANN_ERR_UNSUPPORTED, "graph degree R > 64 is not supported by the wave64 kernels");
+  if (h->layout.dim > 256)
+    raise(GANN_ERR_UNSUPPORTED, "dim > 256 is not supported by the register rerank");
 }
 
 // Entry selection (src/pure_mem.cu:104-124): nav kernel + on-device
@@ -402,9 +409,8 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
   if (mode != GANN_MODE_STEPWISE) raise(GANN_ERR_INVALID, "unknown mode");
   // step-wise: LUTs in HBM, one launch per expansion round, host polls the
   // active count (the request[] round trip of src/hyd_task_runner.cu:126-178)
-  const int64_t cap = L + Ly.max_m;
   h->luts.ensure((size_t)nq * h->pq.dev.M * gann::kNumPivots * 4);
-  h->lists.ensure((size_t)nq * cap * 8);
+  h->lists.ensure((size_t)nq * L * 8);
   h->state.ensure((size_t)nq * gann::step_state_bytes());
   h->counters.ensure(64);
   GANN_HIP(gann::launch_step_init(h->pq.dev, q_dev, nq, entries, h->luts.as<float>(), h->state.p, s));

@@ -205,23 +205,33 @@ __global__ __launch_bounds__(64) void nav_entry_kernel(NavDev nav, int64_t medoi
 
 // ------------------------------------------------------------------ beam search
 
-// Per-expansion step shared by the fused and the step-wise kernels.
-// State in LDS: list A (sorted, distinct masked ids, visited bit in bit 31
-// of the low word), scratch B (merge target), N (sorted new run).
-// Returns the next node (or -1) and updates *sz.
-struct StepCtx {
-  uint64_t* A;
-  uint64_t* B;
-  uint64_t* N;
-  int L;
-};
-
-// Lower bound of `key` in a[0..n) compared by entry_key (first element whose
-// key is not below `key`).
+// Per-expansion list update shared by the fused and the step-wise kernels.
+//
+// The reference (src/impl/pure_mem.cuh:350-419) merges the sorted new run
+// into the list by merge-path ranks, caps the result at 2L, removes every
+// entry whose id equals its predecessor's (a new copy always lands right
+// after its old copy, :358-360), caps at L and takes the first unvisited
+// entry below L.  The same list results from inserting only the new entries
+// that are not already present:
+//  * the 2L cap never changes the first L distinct entries (each id occurs
+//    at most twice among the first 2L merged entries), so it is dropped;
+//  * a new entry is a duplicate iff the old entry at its lower bound has the
+//    same id; the others move in at rank + (earlier inserted count);
+//  * an old entry i moves right by the number of inserted entries ranked at
+//    or before i;
+//  * every entry before the first unvisited one is visited, so the next
+//    node is min(new position of the old first-unvisited entry, position of
+//    the first inserted entry), tracked incrementally in fu.
+// The update runs in two phases so the caller can start fetching the next
+// node's record between them: plan() ranks the new run and picks the next
+// node without writing; apply() shifts the list in place (top chunk first,
+// skipping everything below the first insertion) and marks the node visited.
+// A: the list (sorted by key, distinct ids, visited flag in bit 31 of the low
+// word), capacity >= L; NR: 64-int scratch.
 __device__ __forceinline__ int lower_bound_entries(const uint64_t* a, int n, uint64_t key) {
   int lo = 0, hi = n;
   while (lo < hi) {
-    int mid = (lo + hi) >> 1;
+    const int mid = (lo + hi) >> 1;
     if (entry_key(a[mid]) < key)
       lo = mid + 1;
     else
@@ -230,65 +240,101 @@ __device__ __forceinline__ int lower_bound_entries(const uint64_t* a, int n, uin
   return lo;
 }
 
-// Merge the sorted new run N[0..deg) (held one per lane in `nkey`) into
-// A[0..sz) as src/impl/pure_mem.cuh:350-377 does, dedup + select as :380-419.
-// Returns the selected node id or -1; *sz is the new list size.
-__device__ __forceinline__ int32_t merge_dedup_select(const StepCtx& c, uint64_t nkey, int deg,
-                                                      int* sz_io) {
+// Number of entries <= x in the sorted int array a[0..n).
+__device__ __forceinline__ int upper_bound_i32(const int32_t* a, int n, int x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] <= x)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+struct ListPlan {
+  uint64_t nkey;  // this lane's new key
+  int r;          // its rank in the old list
+  int p;          // its position in the new list (or -1: duplicate)
+  int n_nd;       // inserted count (uniform)
+  int p0;         // position of the first inserted entry (uniform, INT_MAX if none)
+  int cand;       // position of the next node in the new list (uniform, -1: stop)
+  uint64_t sel;   // the selected entry (uniform)
+  int nsz;        // new list size (uniform)
+};
+
+__device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int32_t* NR, int L, uint64_t nkey,
+                                              int deg, int sz, int fu) {
   const int lane = lane_id();
-  const int sz = *sz_io;
-  const int L = c.L;
-  // new item rank: lower_bound in the old list, +1 if that slot holds the
-  // same id (the new copy goes right after the old one) (:351-361)
+  ListPlan P;
+  P.nkey = nkey;
+  int r = 0;
+  bool nd = false;
   if (lane < deg) {
-    c.N[lane] = nkey;
-    int r = lower_bound_entries(c.A, sz, nkey);
-    if (r < sz && ((entry_id(c.A[r]) ^ (uint32_t)nkey) & kMask31) == 0) ++r;
-    c.B[r + lane] = nkey;
+    r = lower_bound_entries(A, sz, nkey);
+    nd = !(r < sz && ((entry_id(A[r]) ^ (uint32_t)nkey) & kMask31) == 0);
   }
-  __syncthreads();
-  // old item rank: lower_bound in the new run (:363-369)
-  for (int i = lane; i < sz; i += kWave) {
-    const uint64_t e = c.A[i];
-    c.B[i + lower_bound_entries(c.N, deg, entry_key(e))] = e;
+  const uint64_t ndm = ballot64(nd);
+  const int e = rank_below(ndm);
+  P.r = r;
+  P.n_nd = __popcll(ndm);
+  P.p = nd ? r + e : -1;
+  if (nd) NR[e] = r;
+  P.p0 = P.n_nd ? __shfl(r, (int)__builtin_ctzll(ndm), kWave) : INT_MAX;
+  P.nsz = min(sz + P.n_nd, L);
+  int fu_new = INT_MAX;
+  uint64_t fu_entry = 0;
+  if (fu < sz) {
+    fu_new = fu + __popcll(ballot64(nd && r <= fu));
+    fu_entry = A[fu];
   }
-  __syncthreads();
-  const int sz2 = min(sz + deg, 2 * L);  // (:377)
-  // dedup adjacent equal ids, compact into A, first unvisited (:380-419)
-  int count = 0;
-  int sel = -1;
-  for (int base = 0; base < sz2; base += kWave) {
-    const int i = base + lane;
-    const bool in = i < sz2;
-    uint64_t e = 0;
-    bool flag = false;
-    if (in) {
-      e = c.B[i];
-      if (i > 0) flag = ((entry_id(c.B[i - 1]) ^ entry_id(e)) & kMask31) == 0;
-    }
-    const uint64_t fmask = ballot64(in && flag);
-    const int mv = i - count - rank_below(fmask);
-    if (in && !flag) c.A[mv] = e;
-    const uint64_t cand = ballot64(in && !flag && !(entry_id(e) & kVisited));
-    if (sel < 0 && cand) {
-      const int first = (int)__builtin_ctzll(cand);
-      sel = __shfl(mv, first, kWave);
-    }
-    count += __popcll(fmask);
-  }
-  __syncthreads();
-  int32_t next = -1;
-  if (sel >= 0 && sel < L) {
-    const uint64_t e = c.A[sel];
-    next = (int32_t)(entry_id(e) & kMask31);
-    *sz_io = min(sz2 - count, L);
-    __syncthreads();
-    if (lane == 0) c.A[sel] = e | kVisited;
+  const int cand = min(fu_new, P.p0);
+  if (cand >= P.nsz) {
+    P.cand = -1;
+    P.sel = 0;
   } else {
-    *sz_io = min(sz2 - count, L);
+    P.cand = cand;
+    P.sel = cand == fu_new ? fu_entry : __shfl(nkey, (int)__builtin_ctzll(ndm), kWave);
   }
+  return P;
+}
+
+// Applies the plan in place; returns the new first-unvisited index.
+__device__ __forceinline__ int list_apply(uint64_t* A, const int32_t* NR, int L, int sz,
+                                          const ListPlan& P) {
+  const int lane = lane_id();
+  __syncthreads();  // NR and all reads of plan() done
+  if (P.n_nd > 0) {
+    const int lo_chunk = (min(P.p0, sz) / kWave) * kWave;
+    for (int base = ((sz - 1) / kWave) * kWave; base >= lo_chunk && sz > 0; base -= kWave) {
+      const int i = base + lane;
+      uint64_t v = 0;
+      int d = -1;
+      if (i < sz) {
+        v = A[i];
+        d = i + upper_bound_i32(NR, P.n_nd, i);
+      }
+      __syncthreads();
+      if (d >= 0 && d < L && d != i) A[d] = v;
+      __syncthreads();
+    }
+    if (P.p >= 0 && P.p < L) A[P.p] = P.nkey;
+    __syncthreads();
+  }
+  if (P.cand < 0) return P.nsz;
+  if (lane == 0) A[P.cand] = P.sel | kVisited;
   __syncthreads();
-  return next;
+  int nfu = P.nsz;
+  for (int base = P.cand + 1; base < P.nsz; base += kWave) {
+    const int i = base + lane;
+    const uint64_t m = ballot64(i < P.nsz && !(entry_id(A[i]) & kVisited));
+    if (m) {
+      nfu = base + (int)__builtin_ctzll(m);
+      break;
+    }
+  }
+  return nfu;
 }
 
 // Top-k insertion of (d, id) into the sorted LDS list (src/impl/util.cuh:116-163):
@@ -334,19 +380,63 @@ __device__ __forceinline__ void topk_push(float* td, int32_t* ti, int* found, in
   __syncthreads();
 }
 
-template <typename T>
 __device__ __forceinline__ const uint8_t* record_of(const IndexDev& ix, int64_t u) {
   return ix.pages + (u / ix.nodes_per_page) * 4096 + (u % ix.nodes_per_page) * ix.node_len;
 }
 
-// LDS carve-up of the fused kernel (bytes): LUT | qr | A | B | N | topk dist | topk id
+// One node record held in registers: its degree, this lane's neighbour id
+// and, in lanes 0..31, the coordinates l, l+32, ... that the exact rerank of
+// lane l reads (square_sum_32's lane roles).  Loads are issued by load() and
+// consumed one expansion later, so their latency overlaps the list update.
+template <typename T, int kPer>
+struct RecRegs {
+  int deg_raw;
+  uint32_t v;
+  T x[kPer];
+  __device__ __forceinline__ void load(const IndexDev& ix, int64_t u) {
+    const int lane = lane_id();
+    const uint8_t* rec = record_of(ix, u);
+    deg_raw = *reinterpret_cast<const int32_t*>(rec + ix.data_len);
+    const uint32_t* edge = reinterpret_cast<const uint32_t*>(rec + ix.data_len + 4);
+    v = lane < ix.R ? edge[lane] : 0u;
+    const T* xs = reinterpret_cast<const T*>(rec);
+    const int l = lane & 31;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = l + 32 * k;
+      x[k] = i < ix.dim ? xs[i] : T(0);
+    }
+  }
+  // square_sum_32 (src/impl/util.cuh:26-46) from the registers: lane l's
+  // partial over dims l, l+32, ... then the 16/8/4/2/1 tree read at lane 0.
+  __device__ __forceinline__ float l2(const float* q, int dim) const {
+    const int l = lane_id() & 31;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = l + 32 * k;
+      if (i < dim) {
+        const float d = q[i] - to_f(x[k]);
+        acc = fma_f(d, d, acc);
+      }
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 32);
+    return __shfl(acc, 0, kWave);
+  }
+};
+
+// LDS carve-up of the fused kernel (bytes): LUT | qr | list A (L) | NR (64
+// ints) | top-k dists | top-k ids.
 struct SearchSmem {
   static __host__ __device__ size_t bytes(int M, int dim, int L, int R, int k) {
-    size_t cap = (size_t)(L + R);
-    return (size_t)M * kPivots * 4 + (size_t)((dim + 1) & ~1) * 4 + cap * 8 * 2 + kWave * 8 +
+    (void)R;
+    return (size_t)M * kPivots * 4 + (size_t)((dim + 1) & ~1) * 4 + (size_t)L * 8 + kWave * 4 +
            (size_t)k * 8;
   }
 };
+
+constexpr int kMaxDimRegs = 8;  // rerank coordinates per lane: dim <= 256
 
 template <typename T, int MW, int W>
 __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
@@ -365,10 +455,13 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   float* lut = reinterpret_cast<float*>(smem_raw);
   float* qr = lut + M * kPivots;
   uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
-  uint64_t* B = A + (L + R);
-  uint64_t* N = B + (L + R);
-  float* td = reinterpret_cast<float*>(N + kWave);
+  int32_t* NR = reinterpret_cast<int32_t*>(A + L);
+  float* td = reinterpret_cast<float*>(NR + kWave);
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
+
+  int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
+  RecRegs<T, kMaxDimRegs> cur;
+  if (u >= 0) cur.load(ix, u);
 
   // q - mu into qr for the LUT build, then the restored query
   // fl(fl(q - mu) + mu) that the reference's rerank reads (src/impl/pq.cuh:22-24, 54-56)
@@ -380,34 +473,33 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   for (int i = lane; i < dim; i += kWave) qr[i] = qr[i] + pq.centroid[i];
   __syncthreads();
 
-  StepCtx c{A, B, N, L};
-  int sz = 0;
-  int found = 0;
-  int32_t u = entries[qi];
+  int sz = 0, fu = 0, found = 0;
   int32_t exps = 0, adcs = 0;
   const int64_t cap = ix.num_pts + 2;
   while (u >= 0 && exps < cap) {
     ++exps;
-    const uint8_t* rec = record_of<T>(ix, u);
-    int deg = *reinterpret_cast<const int32_t*>(rec + ix.data_len);
-    deg = __builtin_amdgcn_readfirstlane(min(max(deg, 0), R));
+    const int deg = __builtin_amdgcn_readfirstlane(min(max(cur.deg_raw, 0), R));
     adcs += deg;
-    const uint32_t* edge = reinterpret_cast<const uint32_t*>(rec + ix.data_len + 4);
-    uint32_t v = 0;
     uint64_t key = ~(uint64_t)0;  // padding sorts last
     if (lane < deg) {
-      v = edge[lane];
       CodeRow<MW> row;
-      const uint8_t* crow = pq.codes + (int64_t)v * M;
+      const uint8_t* crow = pq.codes + (int64_t)cur.v * M;
       row.load(crow, M);
-      key = make_key(row.adc(lut, crow, M), v);
+      key = make_key(row.adc(lut, crow, M), cur.v);
     }
     // exact rerank of u (independent of the list update; :420-423)
-    const float du = l2_square_sum_32<T>(qr, reinterpret_cast<const T*>(rec), dim);
+    const float du = cur.l2(qr, dim);
     key = wave_sort64(key);
-    const int32_t next = merge_dedup_select(c, key, deg, &sz);
+    const ListPlan P = list_plan(A, NR, L, key, deg, sz, fu);
+    const int32_t next =
+        __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1);
+    RecRegs<T, kMaxDimRegs> nxt;
+    if (next >= 0) nxt.load(ix, next);
+    fu = list_apply(A, NR, L, sz, P);
+    sz = P.nsz;
     topk_push(td, ti, &found, topk, du, u);
-    u = __builtin_amdgcn_readfirstlane(next);
+    u = next;
+    cur = nxt;
   }
   // results; slots past found stay 0 as in the reference's zero-initialised vectors
   for (int j = lane; j < topk; j += kWave) {
@@ -430,6 +522,7 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
 struct StepState {
   int32_t u;      // node to expand this round, -1 when done
   int32_t sz;     // list size
+  int32_t fu;     // index of the first unvisited list entry (sz if none)
   int32_t found;  // top-k fill
   int32_t exps;   // expansions so far
   int32_t adcs;   // ADC evaluations so far
@@ -449,7 +542,7 @@ __global__ __launch_bounds__(64) void step_init_kernel(PQDev pq, const float* __
   for (int i = lane; i < pq.dim; i += kWave) qs[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
   __syncthreads();
   lut_build<W>(pq, qs, luts + (int64_t)qi * pq.M * kPivots, lane, kWave);
-  if (lane == 0) st[qi] = StepState{entries[qi], 0, 0, 0, 0};
+  if (lane == 0) st[qi] = StepState{entries[qi], 0, 0, 0, 0, 0};
 }
 
 // One expansion per active query: the work of merge_data_kernel followed by
@@ -471,19 +564,20 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
   if (s.u < 0) return;
   const int lane = lane_id();
   const int dim = ix.dim, M = pq.M, R = ix.R;
-  const int cap = L + R;
   float* qr = reinterpret_cast<float*>(smem_raw);
   uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
-  uint64_t* B = A + cap;
-  uint64_t* N = B + cap;
-  float* td = reinterpret_cast<float*>(N + kWave);
+  int32_t* NR = reinterpret_cast<int32_t*>(A + L);
+  float* td = reinterpret_cast<float*>(NR + kWave);
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
   const float* lut = luts + (int64_t)qi * M * kPivots;
-  uint64_t* glist = lists + (int64_t)qi * cap;
+  uint64_t* glist = lists + (int64_t)qi * L;
 
+  const int32_t u = __builtin_amdgcn_readfirstlane(s.u);
+  RecRegs<T, kMaxDimRegs> cur;
+  cur.load(ix, u);
   const float* qq = q + (int64_t)qi * dim;
   for (int i = lane; i < dim; i += kWave) {
-    float t = qq[i] - pq.centroid[i];
+    const float t = qq[i] - pq.centroid[i];
     qr[i] = t + pq.centroid[i];
   }
   for (int i = lane; i < s.sz; i += kWave) A[i] = glist[i];
@@ -493,24 +587,20 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
   }
   __syncthreads();
 
-  const int32_t u = s.u;
-  const uint8_t* rec = record_of<T>(ix, u);
-  int deg = *reinterpret_cast<const int32_t*>(rec + ix.data_len);
-  deg = __builtin_amdgcn_readfirstlane(min(max(deg, 0), R));
-  const uint32_t* edge = reinterpret_cast<const uint32_t*>(rec + ix.data_len + 4);
+  const int deg = __builtin_amdgcn_readfirstlane(min(max(cur.deg_raw, 0), R));
   uint64_t key = ~(uint64_t)0;
   if (lane < deg) {
-    const uint32_t v = edge[lane];
     CodeRow<MW> row;
-    const uint8_t* crow = pq.codes + (int64_t)v * M;
+    const uint8_t* crow = pq.codes + (int64_t)cur.v * M;
     row.load(crow, M);
-    key = make_key(row.adc(lut, crow, M), v);
+    key = make_key(row.adc(lut, crow, M), cur.v);
   }
-  const float du = l2_square_sum_32<T>(qr, reinterpret_cast<const T*>(rec), dim);
+  const float du = cur.l2(qr, dim);
   key = wave_sort64(key);
-  StepCtx c{A, B, N, L};
-  int sz = s.sz;
-  const int32_t next = merge_dedup_select(c, key, deg, &sz);
+  const ListPlan P = list_plan(A, NR, L, key, deg, s.sz, s.fu);
+  const int32_t next = P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1;
+  const int fu = list_apply(A, NR, L, s.sz, P);
+  const int sz = P.nsz;
   int found = s.found;
   topk_push(td, ti, &found, topk, du, u);
 
@@ -522,7 +612,7 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
   if (lane == 0) {
     const int32_t exps = s.exps + 1;
     const bool done = next < 0 || exps >= ix.num_pts + 2;
-    st[qi] = StepState{done ? -1 : next, sz, found, exps, s.adcs + deg};
+    st[qi] = StepState{done ? -1 : next, sz, fu, found, exps, s.adcs + deg};
     if (done) atomicSub(active, 1);
   }
 }
@@ -647,8 +737,7 @@ template <typename T>
 hipError_t launch_round_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
                           const float* luts, int topk, int L, uint64_t* lists, StepState* st,
                           int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
-  const size_t cap = (size_t)(L + ix.R);
-  const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + cap * 16 + kWave * 8 + (size_t)topk * 8;
+  const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + (size_t)L * 8 + kWave * 4 + (size_t)topk * 8;
   return with_mw(pq.M, [&](auto mw) {
     hipLaunchKernelGGL((step_round_kernel<T, decltype(mw)::value>), dim3(nq), dim3(64), smem,
                        stream, ix, pq, q, nq, luts, topk, L, lists, st, nns, dists, active);

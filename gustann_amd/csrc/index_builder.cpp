@@ -121,16 +121,23 @@ struct Cand {
   bool operator<(const Cand& o) const { return d < o.d || (d == o.d && id < o.id); }
 };
 
+// Adjacency with slack: a list may grow to C = ceil(1.3 R) entries through
+// reverse edges before it is pruned back to R (DiskANN's graph slack), so
+// that most reverse insertions do not trigger a prune.
 struct Graph {
-  int64_t n, R;
-  std::vector<uint32_t> nbr;  // [n][R]
+  int64_t n, R, C;
+  std::vector<uint32_t> nbr;  // [n][C]
   std::vector<uint32_t> deg;  // [n]
   std::vector<std::mutex> locks;
-  Graph(int64_t n_, int64_t R_) : n(n_), R(R_), nbr((size_t)(n_ * R_)), deg((size_t)n_, 0), locks((size_t)n_) {}
+  Graph(int64_t n_, int64_t R_)
+      : n(n_), R(R_), C((R_ * 13 + 9) / 10), nbr((size_t)(n_ * ((R_ * 13 + 9) / 10))),
+        deg((size_t)n_, 0), locks((size_t)n_) {}
+  uint32_t* row(int64_t u) { return nbr.data() + u * C; }
+  const uint32_t* row(int64_t u) const { return nbr.data() + u * C; }
 };
 
-// Greedy best-first search with a sorted list of size L; returns every node
-// whose distance was computed (the "visited" pool used for pruning).
+// Greedy best-first search with a sorted list of size L; `pool` receives the
+// expanded nodes (DiskANN's visited set used as pruning candidates).
 struct Searcher {
   std::vector<uint32_t> tag;
   uint32_t epoch = 0;
@@ -150,7 +157,6 @@ struct Searcher {
       if (tag[v] == epoch) return;
       tag[v] = epoch;
       Cand c{P.dist(q, v), v};
-      pool.push_back(c);
       if ((int64_t)list.size() == L && !(c < list.back())) return;
       auto it = std::lower_bound(list.begin(), list.end(), c);
       size_t pos = (size_t)(it - list.begin());
@@ -170,9 +176,10 @@ struct Searcher {
       }
       expanded[i] = 1;
       uint32_t u = list[i].id;
+      pool.push_back(list[i]);
       {
         std::lock_guard<std::mutex> g(const_cast<Graph&>(G).locks[u]);
-        snapshot.assign(G.nbr.begin() + (long)(u * G.R), G.nbr.begin() + (long)(u * G.R + G.deg[u]));
+        snapshot.assign(G.row(u), G.row(u) + G.deg[u]);
       }
       size_t before = i;
       for (uint32_t v : snapshot) push(v);
@@ -188,10 +195,12 @@ struct Searcher {
 // alpha-dominates, repeat until R are kept.
 void robust_prune(const Points& P, int64_t p, std::vector<Cand>& cand, float alpha, int64_t R,
                   std::vector<uint32_t>& out) {
+  constexpr size_t kMaxCand = 750;  // DiskANN's maxc
   std::sort(cand.begin(), cand.end());
   cand.erase(std::unique(cand.begin(), cand.end(),
                          [](const Cand& a, const Cand& b) { return a.id == b.id; }),
              cand.end());
+  if (cand.size() > kMaxCand) cand.resize(kMaxCand);
   out.clear();
   std::vector<float> occl(cand.size(), 0.f);
   for (size_t i = 0; i < cand.size() && (int64_t)out.size() < R; ++i) {
@@ -245,7 +254,7 @@ void vamana(const Points& P, int64_t R, int64_t L, float alpha, uint64_t seed, i
 #pragma omp parallel for num_threads(nthreads) schedule(static)
   for (int64_t u = 0; u < n; ++u) {
     Rng r(seed, (uint64_t)u + 1);
-    uint32_t* out = G.nbr.data() + u * R;
+    uint32_t* out = G.row(u);
     int64_t k = 0;
     while (k < init_deg) {
       uint32_t v = (uint32_t)r.below((uint64_t)n);
@@ -262,13 +271,25 @@ void vamana(const Points& P, int64_t R, int64_t L, float alpha, uint64_t seed, i
     std::mt19937_64 g(seed ^ 0x5eedull);
     std::shuffle(order.begin(), order.end(), g);
   }
+  auto prune_row = [&](int64_t v, float a, std::vector<uint32_t>& vp) {
+    std::vector<Cand> vc;
+    {
+      std::lock_guard<std::mutex> g(G.locks[(size_t)v]);
+      const uint32_t* vn = G.row(v);
+      for (uint32_t j = 0; j < G.deg[(size_t)v]; ++j) vc.push_back(Cand{P.dist(v, vn[j]), vn[j]});
+    }
+    robust_prune(P, v, vc, a, R, vp);
+    std::lock_guard<std::mutex> g(G.locks[(size_t)v]);
+    std::copy(vp.begin(), vp.end(), G.row(v));
+    G.deg[(size_t)v] = (uint32_t)vp.size();
+  };
   const float alphas[2] = {1.0f, alpha};
   for (float a : alphas) {
 #pragma omp parallel num_threads(nthreads)
     {
       Searcher S(n);
       std::vector<Cand> cand;
-      std::vector<uint32_t> pruned, nb;
+      std::vector<uint32_t> pruned, vp;
 #pragma omp for schedule(dynamic, 64)
       for (int64_t oi = 0; oi < n; ++oi) {
         int64_t p = order[(size_t)oi];
@@ -276,50 +297,44 @@ void vamana(const Points& P, int64_t R, int64_t L, float alpha, uint64_t seed, i
         cand = S.pool;
         {
           std::lock_guard<std::mutex> g(G.locks[(size_t)p]);
-          for (uint32_t j = 0; j < G.deg[(size_t)p]; ++j) {
-            uint32_t v = G.nbr[(size_t)(p * R + j)];
-            cand.push_back(Cand{P.dist(p, v), v});
-          }
+          const uint32_t* pn = G.row(p);
+          for (uint32_t j = 0; j < G.deg[(size_t)p]; ++j) cand.push_back(Cand{P.dist(p, pn[j]), pn[j]});
         }
         robust_prune(P, p, cand, a, R, pruned);
         {
           std::lock_guard<std::mutex> g(G.locks[(size_t)p]);
-          std::copy(pruned.begin(), pruned.end(), G.nbr.begin() + (long)(p * R));
+          std::copy(pruned.begin(), pruned.end(), G.row(p));
           G.deg[(size_t)p] = (uint32_t)pruned.size();
         }
-        // reverse edges
+        // reverse edges; a list that overflows its slack is pruned back to R
         for (uint32_t v : pruned) {
           bool need_prune = false;
           {
             std::lock_guard<std::mutex> g(G.locks[v]);
-            uint32_t* vn = G.nbr.data() + (int64_t)v * R;
+            uint32_t* vn = G.row(v);
             uint32_t dv = G.deg[v];
             bool present = false;
             for (uint32_t j = 0; j < dv; ++j) present |= vn[j] == (uint32_t)p;
             if (!present) {
-              if ((int64_t)dv < R) {
+              if ((int64_t)dv < G.C) {
                 vn[dv] = (uint32_t)p;
-                G.deg[v] = dv + 1;
-              } else {
-                need_prune = true;
-                nb.assign(vn, vn + dv);
+                G.deg[v] = ++dv;
               }
+              need_prune = (int64_t)dv >= G.C;
             }
           }
-          if (need_prune) {
-            std::vector<Cand> vc;
-            vc.reserve(nb.size() + 1);
-            for (uint32_t w : nb) vc.push_back(Cand{P.dist(v, w), w});
-            vc.push_back(Cand{P.dist(v, p), (uint32_t)p});
-            std::vector<uint32_t> vp;
-            robust_prune(P, v, vc, a, R, vp);
-            std::lock_guard<std::mutex> g(G.locks[v]);
-            std::copy(vp.begin(), vp.end(), G.nbr.begin() + (long)((int64_t)v * R));
-            G.deg[v] = (uint32_t)vp.size();
-          }
+          if (need_prune) prune_row(v, a, vp);
         }
       }
     }
+  }
+  // final pass: every list back to at most R
+#pragma omp parallel num_threads(nthreads)
+  {
+    std::vector<uint32_t> vp;
+#pragma omp for schedule(dynamic, 256)
+    for (int64_t v = 0; v < n; ++v)
+      if ((int64_t)G.deg[(size_t)v] > R) prune_row(v, alpha, vp);
   }
 }
 
@@ -553,8 +568,10 @@ int gib_vamana(const void* data, int64_t n, int64_t dim, int dtype, int64_t R, i
   int64_t med = find_medoid(P, nthreads);
   Graph G(n, R);
   vamana(P, R, L, alpha, seed, nthreads, G, med);
-  std::memcpy(out_nbr, G.nbr.data(), sizeof(uint32_t) * (size_t)(n * R));
-  std::memcpy(out_deg, G.deg.data(), sizeof(uint32_t) * (size_t)n);
+  for (int64_t u = 0; u < n; ++u) {
+    std::memcpy(out_nbr + u * R, G.row(u), sizeof(uint32_t) * (size_t)G.deg[(size_t)u]);
+    out_deg[u] = G.deg[(size_t)u];
+  }
   *out_medoid = med;
   return 0;
 }

@@ -243,6 +243,7 @@ class DatasetSpec:
     nav_R: int = 32
     nav_L: int = 50
     zipf_s: float = 0.0           # > 0: query clusters ~ Zipf(s)
+    gt_nq: int = 0                # ground truth for the first gt_nq queries (0 = all)
     seed: int = 1234
     extra: dict = field(default_factory=dict)
 
@@ -251,6 +252,7 @@ def build_dataset(spec: DatasetSpec, out_dir: str, threads=None, verbose=False) 
     """Generates data, builds the Vamana graph, PQ and (optionally) the pivot
     graph, computes ground truth and writes everything under out_dir.
     Returns a dict of paths and metadata (also saved as meta.json)."""
+    import sys
     import time
     os.makedirs(out_dir, exist_ok=True)
     t0 = time.time()
@@ -269,16 +271,18 @@ def build_dataset(spec: DatasetSpec, out_dir: str, threads=None, verbose=False) 
                                threads=threads)
         Qb = Q
     if verbose:
-        print(f"[{spec.name}] data {time.time() - t0:.1f}s", flush=True)
+        print(f"[{spec.name}] data {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     nbr, deg, med = build_vamana(X, spec.R, spec.L_build, spec.alpha, s + 3, threads)
     if verbose:
-        print(f"[{spec.name}] vamana {time.time() - t0:.1f}s (avg deg {deg.mean():.1f})", flush=True)
+        print(f"[{spec.name}] vamana {time.time() - t0:.1f}s (avg deg {deg.mean():.1f})", file=sys.stderr,
+              flush=True)
     pq = train_pq(X, spec.M, spec.pq_sample, spec.pq_iters, s + 4, threads)
     if verbose:
-        print(f"[{spec.name}] pq {time.time() - t0:.1f}s", flush=True)
-    gt, gtd = brute_force_knn(X, Q, max(spec.k, 10), threads)
+        print(f"[{spec.name}] pq {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    ngt = spec.gt_nq if spec.gt_nq > 0 else spec.nq
+    gt, gtd = brute_force_knn(X, Q[:ngt], max(spec.k, 10), threads)
     if verbose:
-        print(f"[{spec.name}] gt {time.time() - t0:.1f}s", flush=True)
+        print(f"[{spec.name}] gt {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     paths = {
         "index": os.path.join(out_dir, "base_disk.index"),
         "pq": os.path.join(out_dir, "pq"),
