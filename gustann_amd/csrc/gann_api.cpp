@@ -161,7 +161,7 @@ struct gann_pq {
   int device = 0;
   hipStream_t stream = nullptr;
   gann::PQDev dev{};
-  DevBuf pivots_t, centroid, chunk_off, codes;
+  DevBuf pivots, pivots_t, centroid, chunk_off, codes;
   bool codes_borrowed = false;
   // scratch of the host-pointer entry points
   DevBuf q, ids, out;
@@ -180,6 +180,7 @@ struct gann_pq {
     for (int i = 0; i < gann::kNumPivots; ++i)
       for (int j = 0; j < dim; ++j) pt[(size_t)j * gann::kNumPivots + i] = pivots[(size_t)i * dim + j];
     upload(pivots_t, pt.data(), pt.size() * 4);
+    upload(this->pivots, pivots, (size_t)gann::kNumPivots * dim * 4);
     upload(centroid, c, (size_t)dim * 4);
     upload(chunk_off, off, (size_t)(M + 1) * 4);
     dev.dim = dim;
@@ -189,6 +190,7 @@ struct gann_pq {
     for (int m = 0; m <= M && w; ++m)
       if (off[m] != m * w) w = 0;
     dev.chunk_w = w;
+    dev.pivots = this->pivots.as<float>();
     dev.pivots_t = pivots_t.as<float>();
     dev.centroid = centroid.as<float>();
     dev.chunk_off = chunk_off.as<int32_t>();
@@ -219,6 +221,8 @@ void check_lds(size_t bytes, int device, const char* what) {
 
 struct gann_handle {
   int device = 0;
+  int num_cus = 0;
+  size_t lds_limit = 0;
   int dtype = 0;
   int placement = GANN_PLACEMENT_HBM;
   hipStream_t stream = nullptr;
@@ -261,6 +265,13 @@ void open_handle(const gann_config* cfg, gann_handle* h) {
   h->dtype = cfg->dtype;
   h->placement = cfg->placement;
   GANN_HIP(hipSetDevice(h->device));
+  {
+    int cus = 0, lds = 0;
+    GANN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device));
+    GANN_HIP(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device));
+    h->num_cus = cus;
+    h->lds_limit = (size_t)lds;
+  }
   GANN_HIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
   h->pq.device = h->device;
   GANN_HIP(hipStreamCreateWithFlags(&h->pq.stream, hipStreamNonBlocking));
@@ -400,6 +411,19 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
                 int32_t* nexp, int32_t* nadc, hipStream_t s) {
   const gann::DiskLayout& Ly = h->layout;
   if (mode == GANN_MODE_FUSED) {
+    // one workgroup per CU holding the pivot table, as many waves as fit
+    const int waves = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit);
+    if (waves >= 2) {
+      h->counters.ensure(64);
+      const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
+      GANN_HIP(gann::launch_search_cb(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,
+                                      dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
+                                      waves, blocks, s));
+      return;
+    }
+    mode = GANN_MODE_FUSED_LUT;
+  }
+  if (mode == GANN_MODE_FUSED_LUT) {
     check_lds(gann::search_smem_bytes(h->pq.dev.M, (int)Ly.dim, L, (int)Ly.max_m, topk), h->device,
               "fused search");
     GANN_HIP(gann::launch_search(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,

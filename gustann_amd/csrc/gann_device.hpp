@@ -21,6 +21,7 @@ struct PQDev {
   int32_t M;
   int32_t chunk_w;          // > 0: chunk m spans dims [m*chunk_w, (m+1)*chunk_w); 0: irregular
   int64_t num_pts;
+  const float* pivots;      // [256][dim]  (row-major as stored in <pq>_pivots.bin)
   const float* pivots_t;    // [dim][256]  (transposed like src/pq_search.cu:88-93)
   const float* centroid;    // [dim]
   const int32_t* chunk_off; // [M + 1]
@@ -68,6 +69,16 @@ __device__ __forceinline__ uint32_t entry_id(uint64_t e) { return (uint32_t)e; }
 __device__ __forceinline__ float entry_dist(uint64_t e) { return __uint_as_float((uint32_t)(e >> 32)); }
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+// Orders LDS accesses among the lanes of one wavefront (a workgroup barrier
+// would also wait for the other waves of a multi-wave workgroup, which run
+// unrelated queries).  DS instructions of one wave complete in issue order;
+// the fence keeps the compiler from moving accesses across this point.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 

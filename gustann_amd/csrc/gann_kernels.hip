@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <algorithm>
 #include <type_traits>
 
 #include "gann_device.hpp"
@@ -304,7 +305,7 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int32_t* NR, in
 __device__ __forceinline__ int list_apply(uint64_t* A, const int32_t* NR, int L, int sz,
                                           const ListPlan& P) {
   const int lane = lane_id();
-  __syncthreads();  // NR and all reads of plan() done
+  wave_sync();  // NR and all reads of plan() done
   if (P.n_nd > 0) {
     const int lo_chunk = (min(P.p0, sz) / kWave) * kWave;
     for (int base = ((sz - 1) / kWave) * kWave; base >= lo_chunk && sz > 0; base -= kWave) {
@@ -315,16 +316,16 @@ __device__ __forceinline__ int list_apply(uint64_t* A, const int32_t* NR, int L,
         v = A[i];
         d = i + upper_bound_i32(NR, P.n_nd, i);
       }
-      __syncthreads();
+      wave_sync();
       if (d >= 0 && d < L && d != i) A[d] = v;
-      __syncthreads();
+      wave_sync();
     }
     if (P.p >= 0 && P.p < L) A[P.p] = P.nkey;
-    __syncthreads();
+    wave_sync();
   }
   if (P.cand < 0) return P.nsz;
   if (lane == 0) A[P.cand] = P.sel | kVisited;
-  __syncthreads();
+  wave_sync();
   int nfu = P.nsz;
   for (int base = P.cand + 1; base < P.nsz; base += kWave) {
     const int i = base + lane;
@@ -364,12 +365,12 @@ __device__ __forceinline__ void topk_push(float* td, int32_t* ti, int* found, in
         vd = td[j];
         vi = ti[j];
       }
-      __syncthreads();
+      wave_sync();
       if (mv) {
         td[j + 1] = vd;
         ti[j + 1] = vi;
       }
-      __syncthreads();
+      wave_sync();
     }
   }
   if (lane == 0 && pos < k) {
@@ -377,7 +378,7 @@ __device__ __forceinline__ void topk_push(float* td, int32_t* ti, int* found, in
     ti[pos] = id;
   }
   if (n + 1 <= k) *found = n + 1;
-  __syncthreads();
+  wave_sync();
 }
 
 __device__ __forceinline__ const uint8_t* record_of(const IndexDev& ix, int64_t u) {
@@ -511,6 +512,175 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
     found_cnt[qi] = found;
     if (n_exp) n_exp[qi] = exps;
     if (n_adc) n_adc[qi] = adcs;
+  }
+}
+
+// ------------------------------------------------------------------ beam search, shared codebook
+
+// The same search with no per-query LUT: the 256 x dim pivot table sits once
+// in each CU's LDS, shared by up to 16 wavefronts (one query each), and every
+// neighbour's ADC distance is computed directly from the pivots.  For chunk
+// m and code c it accumulates fma((q_i - mu_i) - P[c][i])^2 over the chunk's
+// dims in ascending order from 0 -- exactly the operations that build
+// LUT[m][c] (src/impl/pq.cuh:35-43) -- then sums the chunks in order
+// (src/impl/pure_mem.cuh:306-308), so the distances are bit-identical to the
+// LUT path while a query needs only its list, query vector and top-k in LDS.
+//
+// Pivot rows are stored with their 16-byte groups permuted by
+// g -> g ^ (c & gmask) so the lanes of a wave, which read random rows at
+// the same chunk, spread over the LDS banks.
+
+struct CbSmem {
+  // per-wave bytes: q - mu | restored q | list (L) | NR (64) | top-k d | top-k id
+  static __host__ __device__ size_t wave_bytes(int dim, int L, int k) {
+    size_t b = (size_t)dim * 8 + (size_t)L * 8 + kWave * 4 + (size_t)k * 8;
+    return (b + 15) & ~(size_t)15;
+  }
+  static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * dim * 4; }
+};
+
+__host__ __device__ inline int cb_gmask(int dim) {
+  const int groups = dim / 4;
+  if (dim % 4 != 0) return 0;
+  if (groups % 16 == 0) return 15;
+  if (groups % 8 == 0) return 7;
+  if (groups % 4 == 0) return 3;
+  return 0;
+}
+
+// Float index of element i of pivot row c in the swizzled LDS table.
+__device__ __forceinline__ int cb_index(int c, int i, int dim, int gmask) {
+  return c * dim + ((((i >> 2) ^ (c & gmask)) << 2) | (i & 3));
+}
+
+template <int W, int MW>
+__device__ __forceinline__ float cb_adc(const float* piv, const float* qs, int dim, int gmask,
+                                        const PQDev& pq, const CodeRow<MW>& row,
+                                        const uint8_t* crow) {
+  float dist = 0.0f;
+  const int M = pq.M;
+  auto chunk = [&](int m, uint32_t c) -> float {
+    float acc = 0.0f;
+    if constexpr (W == 4) {
+      const float4 p = *reinterpret_cast<const float4*>(piv + cb_index((int)c, 4 * m, dim, gmask));
+      const float4 qv = *reinterpret_cast<const float4*>(qs + 4 * m);
+      float d;
+      d = qv.x - p.x; acc = fma_f(d, d, acc);
+      d = qv.y - p.y; acc = fma_f(d, d, acc);
+      d = qv.z - p.z; acc = fma_f(d, d, acc);
+      d = qv.w - p.w; acc = fma_f(d, d, acc);
+    } else if constexpr (W == 2) {
+      const float2 p = *reinterpret_cast<const float2*>(piv + cb_index((int)c, 2 * m, dim, gmask));
+      const float2 qv = *reinterpret_cast<const float2*>(qs + 2 * m);
+      float d;
+      d = qv.x - p.x; acc = fma_f(d, d, acc);
+      d = qv.y - p.y; acc = fma_f(d, d, acc);
+    } else {
+      const int lo = pq.chunk_off[m], hi = pq.chunk_off[m + 1];
+      for (int i = lo; i < hi; ++i) {
+        const float d = qs[i] - piv[cb_index((int)c, i, dim, gmask)];
+        acc = fma_f(d, d, acc);
+      }
+    }
+    return acc;
+  };
+  if constexpr (MW > 0) {
+#pragma unroll
+    for (int k = 0; k < MW; ++k) {
+      const uint32_t ws[4] = {row.w[k].x, row.w[k].y, row.w[k].z, row.w[k].w};
+#pragma unroll
+      for (int b = 0; b < 16; ++b) dist = dist + chunk(k * 16 + b, (ws[b >> 2] >> (8 * (b & 3))) & 0xffu);
+    }
+  } else {
+    for (int m = 0; m < M; ++m) dist = dist + chunk(m, crow[m]);
+  }
+  return dist;
+}
+
+template <typename T, int MW, int W>
+__global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
+                                                         const float* __restrict__ q, int nq,
+                                                         const int32_t* __restrict__ entries,
+                                                         int topk, int L, int32_t* __restrict__ nns,
+                                                         float* __restrict__ dists,
+                                                         int32_t* __restrict__ found_cnt,
+                                                         int32_t* __restrict__ n_exp,
+                                                         int32_t* __restrict__ n_adc,
+                                                         int32_t* __restrict__ queue) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  const int dim = ix.dim, M = pq.M, R = ix.R;
+  const int gmask = cb_gmask(dim);
+  float* piv = reinterpret_cast<float*>(smem_raw);
+  // pivot table, swizzled (whole workgroup), the only workgroup barrier
+  for (int idx = threadIdx.x; idx < kPivots * dim; idx += blockDim.x) {
+    const int c = idx / dim, i = idx - c * dim;
+    piv[cb_index(c, i, dim, gmask)] = pq.pivots[idx];
+  }
+  __syncthreads();
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  uint8_t* wbase = smem_raw + CbSmem::pivot_bytes(dim) + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
+  float* qs = reinterpret_cast<float*>(wbase);
+  float* qr = qs + dim;
+  uint64_t* A = reinterpret_cast<uint64_t*>(qr + dim);
+  int32_t* NR = reinterpret_cast<int32_t*>(A + L);
+  float* td = reinterpret_cast<float*>(NR + kWave);
+  int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
+  const int64_t cap = ix.num_pts + 2;
+
+  for (;;) {
+    int qi = 0;
+    if (lane == 0) qi = atomicAdd(queue, 1);
+    qi = __builtin_amdgcn_readfirstlane(__shfl(qi, 0, kWave));
+    if (qi >= nq) break;
+    int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
+    RecRegs<T, kMaxDimRegs> cur;
+    if (u >= 0) cur.load(ix, u);
+    const float* qq = q + (int64_t)qi * dim;
+    for (int i = lane; i < dim; i += kWave) {
+      const float t = qq[i] - pq.centroid[i];  // src/impl/pq.cuh:22-24
+      qs[i] = t;
+      qr[i] = t + pq.centroid[i];             // restored in place, :54-56
+    }
+    wave_sync();
+    int sz = 0, fu = 0, found = 0;
+    int32_t exps = 0, adcs = 0;
+    while (u >= 0 && exps < cap) {
+      ++exps;
+      const int deg = __builtin_amdgcn_readfirstlane(min(max(cur.deg_raw, 0), R));
+      adcs += deg;
+      uint64_t key = ~(uint64_t)0;  // padding sorts last
+      if (lane < deg) {
+        CodeRow<MW> row;
+        const uint8_t* crow = pq.codes + (int64_t)cur.v * M;
+        row.load(crow, M);
+        key = make_key(cb_adc<W, MW>(piv, qs, dim, gmask, pq, row, crow), cur.v);
+      }
+      const float du = cur.l2(qr, dim);
+      key = wave_sort64(key);
+      const ListPlan P = list_plan(A, NR, L, key, deg, sz, fu);
+      const int32_t next =
+          __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1);
+      RecRegs<T, kMaxDimRegs> nxt;
+      if (next >= 0) nxt.load(ix, next);
+      fu = list_apply(A, NR, L, sz, P);
+      sz = P.nsz;
+      topk_push(td, ti, &found, topk, du, u);
+      u = next;
+      cur = nxt;
+    }
+    for (int j = lane; j < topk; j += kWave) {
+      const bool ok = j < found;
+      nns[(int64_t)qi * topk + j] = ok ? ti[j] : 0;
+      dists[(int64_t)qi * topk + j] = ok ? td[j] : 0.0f;
+    }
+    if (lane == 0) {
+      found_cnt[qi] = found;
+      if (n_exp) n_exp[qi] = exps;
+      if (n_adc) n_adc[qi] = adcs;
+    }
+    wave_sync();
   }
 }
 
@@ -754,6 +924,34 @@ hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const f
                                     n_adc, stream);
   return launch_search_t<float>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
                                 stream);
+}
+
+int search_cb_waves(int dim, int L, int topk, size_t lds_limit) {
+  const size_t piv = CbSmem::pivot_bytes(dim), w = CbSmem::wave_bytes(dim, L, topk);
+  if (piv + w > lds_limit) return 0;
+  return (int)std::min<size_t>(16, (lds_limit - piv) / w);
+}
+
+hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                            const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
+                            int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
+                            int waves, int blocks, hipStream_t stream) {
+  const size_t smem = CbSmem::pivot_bytes(ix.dim) + (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
+  hipError_t e = launch_fill_i32(queue, 1, 0, stream);
+  if (e != hipSuccess) return e;
+  auto go = [&](auto t) {
+    using T = decltype(t);
+    return with_mw(pq.M, [&](auto mw) {
+      return with_w(pq.chunk_w, [&](auto w) {
+        hipLaunchKernelGGL((search_cb_kernel<T, decltype(mw)::value, decltype(w)::value>),
+                           dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries,
+                           topk, L, nns, dists, found, n_exp, n_adc, queue);
+        return hipGetLastError();
+      });
+    });
+  };
+  if (dtype == 0) return go(uint8_t{});
+  return go(float{});
 }
 
 size_t step_state_bytes() { return sizeof(StepState); }

@@ -23,6 +23,12 @@ hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_
 hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                          const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                          int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
+// Shared-codebook search: waves per workgroup that fit the LDS (0 = does not fit).
+int search_cb_waves(int dim, int L, int topk, size_t lds_limit);
+hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                            const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
+                            int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
+                            int waves, int blocks, hipStream_t stream);
 hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
                             float* luts, void* st, hipStream_t stream);
 hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,

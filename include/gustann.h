@@ -42,8 +42,10 @@ extern "C" {
 #define GANN_PLACEMENT_HBM 0         /* search_mem -G: index pages copied to HBM */
 #define GANN_PLACEMENT_HOST_PINNED 1 /* search_mem without -G: pages read zero-copy from pinned host memory */
 
-#define GANN_MODE_FUSED 0    /* one persistent kernel per search (src/impl/pure_mem.cuh:243-432) */
-#define GANN_MODE_STEPWISE 1 /* one launch per expansion round, list in HBM (src/impl/hyd_search_v2.cuh) */
+#define GANN_MODE_FUSED 0     /* one kernel per search (src/impl/pure_mem.cuh:243-432); picks the
+                                 shared-codebook kernel when the pivot table fits in LDS */
+#define GANN_MODE_STEPWISE 1  /* one launch per expansion round, list in HBM (src/impl/hyd_search_v2.cuh) */
+#define GANN_MODE_FUSED_LUT 2 /* the fused kernel with a per-query LUT in LDS, forced */
 
 typedef struct gann_handle gann_handle;
 typedef struct gann_pq gann_pq;

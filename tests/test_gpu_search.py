@@ -12,7 +12,8 @@ from _helpers import exact_pq, write_custom_index
 from test_search_semantics import random_graph
 
 import oracle as orc
-from gustann_amd import GannError, GustANN, GustANNConfig, GustANNStats, MODE_STEPWISE, UINT8, FLOAT
+from gustann_amd import (FLOAT, MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, UINT8, GannError, GustANN,
+                         GustANNConfig, GustANNStats)
 from gustann_amd import index as gi
 
 pytestmark = pytest.mark.gpu
@@ -59,13 +60,15 @@ def test_nav_entries_match_oracle(u8):
     assert np.array_equal(ent, [ix.entry(q)[0] for q in Q])
 
 
-@pytest.mark.parametrize("L,topk", [(10, 10), (16, 10), (40, 10), (100, 10), (64, 1), (200, 100)])
-def test_fused_search_matches_oracle_u8(u8, L, topk):
+@pytest.mark.parametrize("mode", [MODE_FUSED, MODE_FUSED_LUT])
+@pytest.mark.parametrize("L,topk", [(10, 10), (16, 10), (40, 10), (100, 10), (64, 1), (200, 100),
+                                    (700, 10)])
+def test_fused_search_matches_oracle_u8(u8, L, topk, mode):
     meta, g, ix = u8
     Q = _queries(meta)
     ne = np.empty(Q.shape[0], np.int32)
     st = GustANNStats()
-    got = g.search(Q, Q.shape[0], topk, L, n_exp=ne, stats=st)
+    got = g.search(Q, Q.shape[0], topk, L, n_exp=ne, stats=st, mode=mode)
     on, od, of, oe, _ = ix.search(Q, topk, L, threads=8)
     _assert_same(got, (on, od, of), ne, oe)
     assert st.n_expansions == int(oe.sum()) and st.n_nav_fallback == 0 and st.run_time > 0
@@ -118,6 +121,8 @@ def test_fused_search_matches_oracle_float(tiny_f32, L):
     _assert_same(got, (on, od, of), ne, oe)
     got2 = g.search(Q, Q.shape[0], 10, L, mode=MODE_STEPWISE)
     _assert_same(got2, (on, od, of))
+    got3 = g.search(Q, Q.shape[0], 10, L, mode=MODE_FUSED_LUT)
+    _assert_same(got3, (on, od, of))
     g.close()
 
 
@@ -134,10 +139,11 @@ def test_random_graphs_match_oracle(tmp_path, seed, R, L, topk, trained):
     g = _open(paths, nav=False)
     ix = orc.Index(*paths[:2])
     Q = rng.integers(0, 256, (40, D)).astype(np.float32)
-    ne = np.empty(40, np.int32)
-    got = g.search(Q, 40, topk, L, n_exp=ne)
     on, od, of, oe, _ = ix.search(Q, topk, L)
-    _assert_same(got, (on, od, of), ne, oe)
+    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE):
+        ne = np.empty(40, np.int32)
+        got = g.search(Q, 40, topk, L, n_exp=ne, mode=mode)
+        _assert_same(got, (on, od, of), ne, oe)
     g.close()
 
 
