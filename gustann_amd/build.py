@@ -75,8 +75,9 @@ def build_cli(verbose=False):
     src = os.path.join(CSRC, "search_mem.cpp")
     if not os.path.exists(src):
         return None
-    _run(["g++", "-O2", "-std=c++17", "-o", out + ".tmp", src, f"-I{os.path.join(ROOT, 'include')}",
-          f"-L{LIB}", "-lgustann_hip", "-Wl,-rpath,$ORIGIN", "-pthread"], verbose)
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-o", out + ".tmp", src,
+          f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}", f"-L{LIB}", "-lgustann_hip",
+          "-Wl,-rpath,$ORIGIN", "-pthread"], verbose)
     os.replace(out + ".tmp", out)
     return out
 

@@ -1,0 +1,60 @@
+"""The search_mem command line (bin/search_disk.cpp flags and output lines)
+over the C ABI: single-L run with the result preview and [REPORT] line, and
+the L-sweep table; recall equals the oracle's on the same index."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from gustann_amd import index as gi
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLI = os.path.join(ROOT, "gustann_amd", "lib", "search_mem")
+
+
+def _run(args):
+    r = subprocess.run([CLI, *args], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stdout
+    return r.stdout
+
+
+def test_single_L_reports_recall(tiny_u8):
+    P = tiny_u8["paths"]
+    out = _run(["--query", P["query"], "--index", P["index"], "--pq_data", P["pq"], "--nav_graph",
+                P["nav"], "--data_type", "uint8", "--ground_truth", P["gt"], "--topk", "10",
+                "--ef_search", "40", "-R", "2", "-G"])
+    m = re.search(r"\[REPORT\] RECALL: ([0-9.]+)", out)
+    assert m and "Recall @ 10:" in out
+    ix = orc.Index(P["index"], P["pq"], P["nav"])
+    Q = gi.read_vecs(P["query"], np.uint8).astype(np.float32)
+    gt = gi.read_vecs(P["gt"], np.int32)
+    nns, _, _, _, _ = ix.search(Q, 10, 40, threads=8)
+    assert abs(float(m.group(1)) - orc.recall(nns, gt, 10)) < 1e-6
+    preview = [l for l in out.splitlines() if "(" in l and "\t" in l]
+    assert len(preview) == 5
+
+
+@pytest.mark.parametrize("mode", ["fused", "lut", "stepwise"])
+def test_sweep_table(tiny_u8, mode):
+    P = tiny_u8["paths"]
+    out = _run(["--query", P["query"], "--index", P["index"], "--pq_data", P["pq"], "--data_type",
+                "uint8", "--ground_truth", P["gt"], "--topk", "10", "--ef_search", "10", "20", "40",
+                "-R", "1", "-G", "--mode", mode])
+    rows = [l.split() for l in out.splitlines()
+            if re.match(r"^\d+\s+[0-9.]+\s+[0-9.]+\s+[0-9.]+$", l.strip())]
+    assert [int(r[0]) for r in rows] == [10, 20, 40]
+    recalls = [float(r[3]) for r in rows]
+    assert recalls[0] <= recalls[1] + 0.02 <= recalls[2] + 0.04
+
+
+def test_rejects_L_below_topk(tiny_u8):
+    P = tiny_u8["paths"]
+    r = subprocess.run([CLI, "--query", P["query"], "--index", P["index"], "--pq_data", P["pq"],
+                        "--data_type", "uint8", "--topk", "10", "--ef_search", "5"],
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=60)
+    assert r.returncode != 0 and "ef_search must be >= topk" in r.stdout
