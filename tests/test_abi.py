@@ -42,3 +42,17 @@ def test_index_builder_library_loads():
     for name in ("gib_vamana", "gib_pq", "gib_brute_force", "gib_write_disk_index",
                  "gib_write_pq", "gib_write_nav", "gib_inspect", "gib_sample_ids"):
         assert hasattr(lib, name)
+
+
+def test_headers_compile_for_c_and_cpp_callers(tmp_path):
+    import subprocess
+    inc = os.path.join(ROOT, "include")
+    c_src = tmp_path / "use.c"
+    c_src.write_text('#include "gustann.h"\nint main(void){gann_handle* h=0; return gann_close(h);}\n')
+    cpp_src = tmp_path / "use.cpp"
+    cpp_src.write_text('#include "gustann.hpp"\nint main(){gustann::GustANN a(gustann::UINT8);'
+                       'gustann::GustANNConfig c; (void)c; return 0;}\n')
+    for cmd in (["gcc", "-std=c11", "-Wall", "-Werror", "-fsyntax-only", f"-I{inc}", str(c_src)],
+                ["g++", "-std=c++17", "-Wall", "-Werror", "-fsyntax-only", f"-I{inc}", str(cpp_src)]):
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        assert r.returncode == 0, r.stdout
