@@ -238,7 +238,7 @@ struct gann_handle {
   DevBuf nav_data, nav_graph, nav_map;
   gann::NavDev nav{};
   // per-call scratch
-  DevBuf q, entries, local, nns, dists, found, nexp, nadc, counters;
+  DevBuf q, entries, local, nns, dists, found, nexp, nadc, counters, qs;
   DevBuf luts, lists, state;
   PinnedBuf counter_host;
 
@@ -415,10 +415,11 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
     const int waves = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit);
     if (waves >= 2) {
       h->counters.ensure(64);
+      h->qs.ensure((size_t)nq * Ly.dim * 4);
       const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
       GANN_HIP(gann::launch_search_cb(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,
                                       dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
-                                      waves, blocks, s));
+                                      h->qs.as<float>(), waves, blocks, s));
       return;
     }
     mode = GANN_MODE_FUSED_LUT;

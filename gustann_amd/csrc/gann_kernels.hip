@@ -241,19 +241,6 @@ __device__ __forceinline__ int lower_bound_entries(const uint64_t* a, int n, uin
   return lo;
 }
 
-// Number of entries <= x in the sorted int array a[0..n).
-__device__ __forceinline__ int upper_bound_i32(const int32_t* a, int n, int x) {
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a[mid] <= x)
-      lo = mid + 1;
-    else
-      hi = mid;
-  }
-  return lo;
-}
-
 struct ListPlan {
   uint64_t nkey;  // this lane's new key
   int r;          // its rank in the old list
@@ -265,8 +252,8 @@ struct ListPlan {
   int nsz;        // new list size (uniform)
 };
 
-__device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int32_t* NR, int L, uint64_t nkey,
-                                              int deg, int sz, int fu) {
+__device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t nkey, int deg,
+                                              int sz, int fu) {
   const int lane = lane_id();
   ListPlan P;
   P.nkey = nkey;
@@ -281,7 +268,6 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int32_t* NR, in
   P.r = r;
   P.n_nd = __popcll(ndm);
   P.p = nd ? r + e : -1;
-  if (nd) NR[e] = r;
   P.p0 = P.n_nd ? __shfl(r, (int)__builtin_ctzll(ndm), kWave) : INT_MAX;
   P.nsz = min(sz + P.n_nd, L);
   int fu_new = INT_MAX;
@@ -301,26 +287,30 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int32_t* NR, in
   return P;
 }
 
-// Applies the plan in place; returns the new first-unvisited index.
-__device__ __forceinline__ int list_apply(uint64_t* A, const int32_t* NR, int L, int sz,
+// Applies the plan in place; returns the new first-unvisited index.  An old
+// entry i moves right by s(i) = (inserted entries ranked below the chunk) +
+// inclusive prefix of the per-chunk histogram H of insertion ranks.
+__device__ __forceinline__ int list_apply(uint64_t* A, int32_t* H, int L, int sz,
                                           const ListPlan& P) {
   const int lane = lane_id();
-  wave_sync();  // NR and all reads of plan() done
+  wave_sync();  // all reads of plan() done
   if (P.n_nd > 0) {
+    const bool ins = P.p >= 0;
     const int lo_chunk = (min(P.p0, sz) / kWave) * kWave;
     for (int base = ((sz - 1) / kWave) * kWave; base >= lo_chunk && sz > 0; base -= kWave) {
       const int i = base + lane;
-      uint64_t v = 0;
-      int d = -1;
-      if (i < sz) {
-        v = A[i];
-        d = i + upper_bound_i32(NR, P.n_nd, i);
-      }
+      const uint64_t v = i < sz ? A[i] : 0;
+      H[lane] = 0;
       wave_sync();
-      if (d >= 0 && d < L && d != i) A[d] = v;
+      if (ins && P.r >= base && P.r < base + kWave) atomicAdd(&H[P.r - base], 1);
+      const int c0 = __popcll(ballot64(ins && P.r < base));
+      wave_sync();
+      const int d = i + c0 + wave_incl_scan(H[lane]);
+      wave_sync();
+      if (i < sz && d < L && d != i) A[d] = v;
       wave_sync();
     }
-    if (P.p >= 0 && P.p < L) A[P.p] = P.nkey;
+    if (ins && P.p < L) A[P.p] = P.nkey;
     wave_sync();
   }
   if (P.cand < 0) return P.nsz;
@@ -410,14 +400,15 @@ struct RecRegs {
   }
   // square_sum_32 (src/impl/util.cuh:26-46) from the registers: lane l's
   // partial over dims l, l+32, ... then the 16/8/4/2/1 tree read at lane 0.
-  __device__ __forceinline__ float l2(const float* q, int dim) const {
+  // qv[k] holds the restored query at dim l + 32k.
+  __device__ __forceinline__ float l2(const float (&qv)[kPer], int dim) const {
     const int l = lane_id() & 31;
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int i = l + 32 * k;
       if (i < dim) {
-        const float d = q[i] - to_f(x[k]);
+        const float d = qv[k] - to_f(x[k]);
         acc = fma_f(d, d, acc);
       }
     }
@@ -438,6 +429,23 @@ struct SearchSmem {
 };
 
 constexpr int kMaxDimRegs = 8;  // rerank coordinates per lane: dim <= 256
+
+// The restored query fl(fl(q - mu) + mu) (src/impl/pq.cuh:22-24, 54-56) in
+// the rerank lane roles: lane l holds dims l, l+32, ...
+__device__ __forceinline__ void restored_query_regs(const float* q, const float* centroid, int dim,
+                                                    float (&qv)[kMaxDimRegs]) {
+  const int l = lane_id() & 31;
+#pragma unroll
+  for (int k = 0; k < kMaxDimRegs; ++k) {
+    const int i = l + 32 * k;
+    float v = 0.0f;
+    if (i < dim) {
+      const float t = q[i] - centroid[i];
+      v = t + centroid[i];
+    }
+    qv[k] = v;
+  }
+}
 
 template <typename T, int MW, int W>
 __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
@@ -464,14 +472,14 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   RecRegs<T, kMaxDimRegs> cur;
   if (u >= 0) cur.load(ix, u);
 
-  // q - mu into qr for the LUT build, then the restored query
-  // fl(fl(q - mu) + mu) that the reference's rerank reads (src/impl/pq.cuh:22-24, 54-56)
+  // q - mu for the LUT build (src/impl/pq.cuh:22-24) and the restored query
+  // the rerank reads
   const float* qq = q + (int64_t)qi * dim;
   for (int i = lane; i < dim; i += kWave) qr[i] = qq[i] - pq.centroid[i];
+  float qv[kMaxDimRegs];
+  restored_query_regs(qq, pq.centroid, dim, qv);
   __syncthreads();
   lut_build<W>(pq, qr, lut, lane, kWave);
-  __syncthreads();
-  for (int i = lane; i < dim; i += kWave) qr[i] = qr[i] + pq.centroid[i];
   __syncthreads();
 
   int sz = 0, fu = 0, found = 0;
@@ -489,9 +497,9 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
       key = make_key(row.adc(lut, crow, M), cur.v);
     }
     // exact rerank of u (independent of the list update; :420-423)
-    const float du = cur.l2(qr, dim);
+    const float du = cur.l2(qv, dim);
     key = wave_sort64(key);
-    const ListPlan P = list_plan(A, NR, L, key, deg, sz, fu);
+    const ListPlan P = list_plan(A, L, key, deg, sz, fu);
     const int32_t next =
         __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1);
     RecRegs<T, kMaxDimRegs> nxt;
@@ -531,9 +539,10 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
 // the same chunk, spread over the LDS banks.
 
 struct CbSmem {
-  // per-wave bytes: q - mu | restored q | list (L) | NR (64) | top-k d | top-k id
+  // per-wave bytes: list (L) | 64-int scratch | top-k d | top-k id
   static __host__ __device__ size_t wave_bytes(int dim, int L, int k) {
-    size_t b = (size_t)dim * 8 + (size_t)L * 8 + kWave * 4 + (size_t)k * 8;
+    (void)dim;
+    size_t b = (size_t)L * 8 + kWave * 4 + (size_t)k * 8;
     return (b + 15) & ~(size_t)15;
   }
   static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * dim * 4; }
@@ -546,6 +555,14 @@ __host__ __device__ inline int cb_gmask(int dim) {
   if (groups % 8 == 0) return 7;
   if (groups % 4 == 0) return 3;
   return 0;
+}
+
+// q - mu of every query (src/impl/pq.cuh:22-24), read back with uniform
+// (scalar) loads by the shared-codebook ADC.
+__global__ void query_centre_kernel(const float* __restrict__ q, const float* __restrict__ centroid,
+                                    int64_t n, int dim, float* __restrict__ qs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) qs[i] = q[i] - centroid[i % dim];
 }
 
 // Float index of element i of pivot row c in the swizzled LDS table.
@@ -606,7 +623,8 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
                                                          int32_t* __restrict__ found_cnt,
                                                          int32_t* __restrict__ n_exp,
                                                          int32_t* __restrict__ n_adc,
-                                                         int32_t* __restrict__ queue) {
+                                                         int32_t* __restrict__ queue,
+                                                         const float* __restrict__ qs_all) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
   const int gmask = cb_gmask(dim);
@@ -621,9 +639,7 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   uint8_t* wbase = smem_raw + CbSmem::pivot_bytes(dim) + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
-  float* qs = reinterpret_cast<float*>(wbase);
-  float* qr = qs + dim;
-  uint64_t* A = reinterpret_cast<uint64_t*>(qr + dim);
+  uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
   int32_t* NR = reinterpret_cast<int32_t*>(A + L);
   float* td = reinterpret_cast<float*>(NR + kWave);
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
@@ -637,13 +653,9 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
     int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
     RecRegs<T, kMaxDimRegs> cur;
     if (u >= 0) cur.load(ix, u);
-    const float* qq = q + (int64_t)qi * dim;
-    for (int i = lane; i < dim; i += kWave) {
-      const float t = qq[i] - pq.centroid[i];  // src/impl/pq.cuh:22-24
-      qs[i] = t;
-      qr[i] = t + pq.centroid[i];             // restored in place, :54-56
-    }
-    wave_sync();
+    const float* qs = qs_all + (int64_t)qi * dim;  // q - mu, uniform reads
+    float qv[kMaxDimRegs];
+    restored_query_regs(q + (int64_t)qi * dim, pq.centroid, dim, qv);
     int sz = 0, fu = 0, found = 0;
     int32_t exps = 0, adcs = 0;
     while (u >= 0 && exps < cap) {
@@ -657,9 +669,9 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
         row.load(crow, M);
         key = make_key(cb_adc<W, MW>(piv, qs, dim, gmask, pq, row, crow), cur.v);
       }
-      const float du = cur.l2(qr, dim);
+      const float du = cur.l2(qv, dim);
       key = wave_sort64(key);
-      const ListPlan P = list_plan(A, NR, L, key, deg, sz, fu);
+      const ListPlan P = list_plan(A, L, key, deg, sz, fu);
       const int32_t next =
           __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1);
       RecRegs<T, kMaxDimRegs> nxt;
@@ -745,11 +757,8 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
   const int32_t u = __builtin_amdgcn_readfirstlane(s.u);
   RecRegs<T, kMaxDimRegs> cur;
   cur.load(ix, u);
-  const float* qq = q + (int64_t)qi * dim;
-  for (int i = lane; i < dim; i += kWave) {
-    const float t = qq[i] - pq.centroid[i];
-    qr[i] = t + pq.centroid[i];
-  }
+  float qv[kMaxDimRegs];
+  restored_query_regs(q + (int64_t)qi * dim, pq.centroid, dim, qv);
   for (int i = lane; i < s.sz; i += kWave) A[i] = glist[i];
   for (int j = lane; j < s.found; j += kWave) {
     td[j] = dists[(int64_t)qi * topk + j];
@@ -765,9 +774,9 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
     row.load(crow, M);
     key = make_key(row.adc(lut, crow, M), cur.v);
   }
-  const float du = cur.l2(qr, dim);
+  const float du = cur.l2(qv, dim);
   key = wave_sort64(key);
-  const ListPlan P = list_plan(A, NR, L, key, deg, s.sz, s.fu);
+  const ListPlan P = list_plan(A, L, key, deg, s.sz, s.fu);
   const int32_t next = P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1;
   const int fu = list_apply(A, NR, L, s.sz, P);
   const int sz = P.nsz;
@@ -935,9 +944,14 @@ int search_cb_waves(int dim, int L, int topk, size_t lds_limit) {
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                            int waves, int blocks, hipStream_t stream) {
+                            float* qs_all, int waves, int blocks, hipStream_t stream) {
   const size_t smem = CbSmem::pivot_bytes(ix.dim) + (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
   hipError_t e = launch_fill_i32(queue, 1, 0, stream);
+  if (e != hipSuccess) return e;
+  const int64_t n = (int64_t)nq * ix.dim;
+  hipLaunchKernelGGL(query_centre_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, q,
+                     pq.centroid, n, ix.dim, qs_all);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   auto go = [&](auto t) {
     using T = decltype(t);
@@ -945,7 +959,7 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
       return with_w(pq.chunk_w, [&](auto w) {
         hipLaunchKernelGGL((search_cb_kernel<T, decltype(mw)::value, decltype(w)::value>),
                            dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries,
-                           topk, L, nns, dists, found, n_exp, n_adc, queue);
+                           topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
         return hipGetLastError();
       });
     });

@@ -28,7 +28,7 @@ int search_cb_waves(int dim, int L, int topk, size_t lds_limit);
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                            int waves, int blocks, hipStream_t stream);
+                            float* qs_all, int waves, int blocks, hipStream_t stream);
 hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
                             float* luts, void* st, hipStream_t stream);
 hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
