@@ -58,14 +58,19 @@ __device__ __forceinline__ float to_f(float v) { return v; }
 // 64-bit ordering key of a candidate: the reference orders by (dist, id with
 // bit 31 masked) (src/impl/util.cuh:166-178).  PQ and L2 distances are sums
 // of squares, hence non-negative, and the IEEE bit pattern of a non-negative
-// float is monotonic in its value, so (bits(dist) << 32 | id & 0x7fffffff)
-// compares exactly like the reference's two-level compare.
+// float is monotonic in its value, so bits(dist) << 32 | (id & 0x7fffffff) << 1
+// compares exactly like the reference's two-level compare.  Bit 0 is free
+// and carries the visited flag of a list entry: a flagged entry still sorts
+// between its own key and the next key, so raw 64-bit compares of entries
+// against fresh keys keep the order and put an entry with the same id at the
+// fresh key's lower bound.
+constexpr uint64_t kListVisited = 1;
 __device__ __forceinline__ uint64_t make_key(float d, uint32_t id) {
-  return ((uint64_t)__float_as_uint(d) << 32) | (uint64_t)(id & kMask31);
+  return ((uint64_t)__float_as_uint(d) << 32) | ((uint64_t)(id & kMask31) << 1);
 }
-// A list entry keeps the visited bit in bit 31 of its low word.
-__device__ __forceinline__ uint64_t entry_key(uint64_t e) { return e & ~(uint64_t)kVisited; }
-__device__ __forceinline__ uint32_t entry_id(uint64_t e) { return (uint32_t)e; }
+__device__ __forceinline__ uint64_t entry_key(uint64_t e) { return e & ~kListVisited; }
+__device__ __forceinline__ uint32_t entry_id(uint64_t e) { return (uint32_t)e >> 1; }
+__device__ __forceinline__ bool entry_visited(uint64_t e) { return (e & kListVisited) != 0; }
 __device__ __forceinline__ float entry_dist(uint64_t e) { return __uint_as_float((uint32_t)(e >> 32)); }
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
@@ -103,30 +108,114 @@ __device__ __forceinline__ int rank_below(uint64_t mask) {
                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  lo = (uint32_t)__shfl_xor((int)lo, m, kWave);
-  hi = (uint32_t)__shfl_xor((int)hi, m, kWave);
-  return ((uint64_t)hi << 32) | lo;
+// Per-lane select by a wave-uniform 64-bit lane mask: lane l gets b if bit l
+// of m is set, else a (one v_cndmask with the mask in scalar registers).
+__device__ __forceinline__ uint32_t lane_select(uint64_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
+  return r;
 }
 
-// Bitonic sort of one 64-bit key per lane, ascending by lane.
-__device__ __forceinline__ uint64_t wave_sort64(uint64_t key) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int k = 2; k <= kWave; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      uint64_t other = shfl_xor_u64(key, j);
-      bool up = (lane & k) == 0;
-      bool lower = (lane & j) == 0;
-      bool take_min = (lower == up);
-      uint64_t mn = other < key ? other : key;
-      uint64_t mx = other < key ? key : other;
-      key = take_min ? mn : mx;
-    }
+// Lanes l with (l & bit) != 0.
+__host__ __device__ constexpr uint64_t lanes_with_bit(int bit) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if (l & bit) m |= 1ull << l;
+  return m;
+}
+
+// Value of v in lane (this lane ^ M) for a compile-time M, on VALU
+// cross-lane paths only (no LDS round trip): DPP quad_perm for 1 and 2, DPP
+// row_shl/row_shr:4 for 4, DPP row_ror:8 for 8 (a rotation by 8 within a
+// 16-lane row is the xor), v_permlane16_swap for 16, v_permlane32_swap for
+// 32.  A swap of v with itself returns {even rows of v duplicated, odd rows
+// of v duplicated}, so the partner row is the other element of the pair.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane xor");
+  const int x = (int)v;
+  if constexpr (M == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, true);  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, true);  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x104, 0xf, 0xf, true);  // lane + 4
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x114, 0xf, 0xf, true);  // lane - 4
+    return lane_select(lanes_with_bit(4), up, dn);
+  } else if constexpr (M == 8) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, true);  // row_ror:8
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return lane_select(lanes_with_bit(16), r[1], r[0]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return lane_select(lanes_with_bit(32), r[1], r[0]);
   }
-  return key;
+}
+
+template <int M>
+__device__ __forceinline__ float xor_lane_f(float v) {
+  return __uint_as_float(xor_lane<M>(__float_as_uint(v)));
+}
+
+// Value of v in lane - 1 (lane 0 keeps its own): DPP wave_shr:1.
+__device__ __forceinline__ uint32_t lane_shr1(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x138, 0xf, 0xf, false);
+}
+
+// Lanes that keep the larger key in the compare-exchange of merge size K,
+// distance J of the bitonic network.
+__host__ __device__ constexpr uint64_t bitonic_max_lanes(int K, int J) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if (((l & K) == 0) != ((l & J) == 0)) m |= 1ull << l;
+  return m;
+}
+
+// One compare-exchange stage on a (64-bit key, 32-bit value) pair per lane.
+// A lane takes its partner's pair when (partner < own) differs from "this
+// lane keeps the larger key"; equal keys (only the ~0 padding) may then
+// duplicate a padding value, which no caller reads.
+template <int K, int J>
+__device__ __forceinline__ void bitonic_step(uint64_t& key, uint32_t& val) {
+  const uint32_t klo = (uint32_t)key, khi = (uint32_t)(key >> 32);
+  const uint32_t olo = xor_lane<J>(klo);
+  const uint32_t ohi = xor_lane<J>(khi);
+  const uint32_t ov = xor_lane<J>(val);
+  const uint64_t other = ((uint64_t)ohi << 32) | olo;
+  const uint64_t sw = ballot64(other < key) ^ bitonic_max_lanes(K, J);
+  key = ((uint64_t)lane_select(sw, khi, ohi) << 32) | lane_select(sw, klo, olo);
+  val = lane_select(sw, val, ov);
+}
+
+template <int K, int J>
+__device__ __forceinline__ void bitonic_merge(uint64_t& key, uint32_t& val) {
+  bitonic_step<K, J>(key, val);
+  if constexpr (J > 1) bitonic_merge<K, J / 2>(key, val);
+}
+
+// Bitonic sort of one (key, value) pair per lane, ascending by key across
+// the 64 lanes.  Keys other than ~0 must be distinct.
+__device__ __forceinline__ void wave_sort64_kv(uint64_t& key, uint32_t& val) {
+  bitonic_merge<2, 1>(key, val);
+  bitonic_merge<4, 2>(key, val);
+  bitonic_merge<8, 4>(key, val);
+  bitonic_merge<16, 8>(key, val);
+  bitonic_merge<32, 16>(key, val);
+  bitonic_merge<64, 32>(key, val);
+}
+
+// The shfl_down tree 16/8/4/2/1 of square_sum_32 (src/impl/util.cuh:36-45)
+// over the partials of lanes 0..31, read at lane 0 and returned to every
+// lane.  The xor butterfly adds the same operand pairs as shfl_down for the
+// lanes that feed lane 0 (l ^ off == l + off for l < off).
+__device__ __forceinline__ float square_sum_tree(float v) {
+  v = v + xor_lane_f<16>(v);
+  v = v + xor_lane_f<8>(v);
+  v = v + xor_lane_f<4>(v);
+  v = v + xor_lane_f<2>(v);
+  v = v + xor_lane_f<1>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
 }
 
 // Exact squared L2 in the order of square_sum_32 (src/impl/util.cuh:26-46):
@@ -143,9 +232,7 @@ __device__ __forceinline__ float l2_square_sum_32(const float* q, const T* x, in
     float d = q[i] - to_f(x[i]);
     v = fma_f(d, d, v);
   }
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v = v + __shfl_xor(v, off, 32);
-  return __shfl(v, 0, kWave);
+  return square_sum_tree(v);
 }
 
 // The same value computed entirely inside one lane (used where every lane

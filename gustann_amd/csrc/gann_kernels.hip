@@ -228,23 +228,40 @@ __global__ __launch_bounds__(64) void nav_entry_kernel(NavDev nav, int64_t medoi
 // node without writing; apply() shifts the list in place (top chunk first,
 // skipping everything below the first insertion) and marks the node visited.
 // A: the list (sorted by key, distinct ids, visited flag in bit 31 of the low
-// word), capacity >= L; NR: 64-int scratch.
-__device__ __forceinline__ int lower_bound_entries(const uint64_t* a, int n, uint64_t key) {
-  int lo = 0, hi = n;
+// word), capacity >= L; BM: list_scratch_words(L) words of scratch.
+
+// Scratch words per wave for the list update: a bitmap of the positions the
+// inserted entries take, two words per 64-entry chunk.
+__host__ __device__ constexpr int list_scratch_words(int L) { return 2 * ((L + kWave - 1) / kWave); }
+
+// Rank of `key` in the sorted list A[0..sz): the number of entries ordered
+// below it.  Each level splits [lo, hi) into 9 segments of s entries and
+// reads the last entry of the first 8 at once; the entries below key form a
+// prefix of those probes, so their count fixes the segment holding the
+// answer.  A 512-entry list takes three dependent LDS reads.
+__device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key, bool active) {
+  int lo = 0, hi = active ? sz : 0;
   while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (entry_key(a[mid]) < key)
-      lo = mid + 1;
-    else
-      hi = mid;
+    const int s = (hi - lo + 8) / 9;
+    int cnt = 0;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) cnt += A[min(lo + s * (m + 1) - 1, hi - 1)] < key ? 1 : 0;
+    const int nhi = cnt == 8 ? hi : min(lo + s * (cnt + 1) - 1, hi - 1);
+    lo = min(lo + s * cnt, hi);
+    hi = nhi;
   }
   return lo;
 }
 
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 struct ListPlan {
-  uint64_t nkey;  // this lane's new key
-  int r;          // its rank in the old list
-  int p;          // its position in the new list (or -1: duplicate)
+  uint64_t nkey;  // lanes 0..n_nd-1: the inserted entries, ascending; other lanes ~0
+  int p;          // lanes 0..n_nd-1: position of the lane's entry in the new list
   int n_nd;       // inserted count (uniform)
   int p0;         // position of the first inserted entry (uniform, INT_MAX if none)
   int cand;       // position of the next node in the new list (uniform, -1: stop)
@@ -252,74 +269,99 @@ struct ListPlan {
   int nsz;        // new list size (uniform)
 };
 
-__device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t nkey, int deg,
+// Ranks each lane's candidate (lanes < deg) in the list, drops those whose id
+// is listed already, sorts the rest with their ranks into lanes 0..n_nd-1
+// (an inserted entry's position is then rank + lane) and picks the next node.
+__device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t key, int deg,
                                               int sz, int fu) {
   const int lane = lane_id();
+  const uint64_t fu_entry = fu < sz ? A[fu] : 0;
+  const bool active = lane < deg;
+  uint32_t r = (uint32_t)list_rank(A, sz, key, active);
+  // a candidate whose id is listed already sits at its lower bound
+  const bool dup = active && (int)r < sz && entry_id(A[r]) == entry_id(key);
+  if (!active || dup) key = ~(uint64_t)0;  // never a real key: ids are < 2^31 - 1
+  wave_sort64_kv(key, r);
   ListPlan P;
-  P.nkey = nkey;
-  int r = 0;
-  bool nd = false;
-  if (lane < deg) {
-    r = lower_bound_entries(A, sz, nkey);
-    nd = !(r < sz && ((entry_id(A[r]) ^ (uint32_t)nkey) & kMask31) == 0);
-  }
-  const uint64_t ndm = ballot64(nd);
-  const int e = rank_below(ndm);
-  P.r = r;
-  P.n_nd = __popcll(ndm);
-  P.p = nd ? r + e : -1;
-  P.p0 = P.n_nd ? __shfl(r, (int)__builtin_ctzll(ndm), kWave) : INT_MAX;
+  P.nkey = key;
+  P.n_nd = __popcll(ballot64(key != ~(uint64_t)0));
+  P.p = (int)r + lane;
+  P.p0 = P.n_nd ? __builtin_amdgcn_readlane((int)r, 0) : INT_MAX;
   P.nsz = min(sz + P.n_nd, L);
   int fu_new = INT_MAX;
-  uint64_t fu_entry = 0;
-  if (fu < sz) {
-    fu_new = fu + __popcll(ballot64(nd && r <= fu));
-    fu_entry = A[fu];
-  }
+  if (fu < sz) fu_new = fu + __popcll(ballot64(lane < P.n_nd && (int)r <= fu));
   const int cand = min(fu_new, P.p0);
   if (cand >= P.nsz) {
     P.cand = -1;
     P.sel = 0;
   } else {
     P.cand = cand;
-    P.sel = cand == fu_new ? fu_entry : __shfl(nkey, (int)__builtin_ctzll(ndm), kWave);
+    P.sel = cand == fu_new ? fu_entry : readlane64(key, 0);
   }
   return P;
 }
 
-// Applies the plan in place; returns the new first-unvisited index.  An old
-// entry i moves right by s(i) = (inserted entries ranked below the chunk) +
-// inclusive prefix of the per-chunk histogram H of insertion ranks.
-__device__ __forceinline__ int list_apply(uint64_t* A, int32_t* H, int L, int sz,
-                                          const ListPlan& P) {
+// Applies the plan in place and returns the new first-unvisited index.  The
+// positions the inserted entries take are marked in the bitmap BM; output
+// position j then holds inserted entry nb(j) (nb = inserted entries placed
+// before j) if marked, else old entry j - nb(j).  Outputs are gathered in
+// batches of 8 chunks, top batch first: a batch reads only positions at or
+// above its lowest output minus 64 and writes after all its reads, so no
+// source is overwritten before it is read.
+__device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListPlan& P) {
+  constexpr int kBatch = 8;
   const int lane = lane_id();
   wave_sync();  // all reads of plan() done
-  if (P.n_nd > 0) {
-    const bool ins = P.p >= 0;
-    const int lo_chunk = (min(P.p0, sz) / kWave) * kWave;
-    for (int base = ((sz - 1) / kWave) * kWave; base >= lo_chunk && sz > 0; base -= kWave) {
-      const int i = base + lane;
-      const uint64_t v = i < sz ? A[i] : 0;
-      H[lane] = 0;
+  const int start = min(P.p0, P.nsz);
+  if (start < P.nsz) {
+    const int ob_lo = (start / kWave) * kWave;
+    const int nch = (P.nsz - ob_lo + kWave - 1) / kWave;
+    const int w_lo = ob_lo / 32;
+    for (int w = lane; w < 2 * nch; w += kWave) BM[w_lo + w] = 0u;
+    wave_sync();
+    if (lane < P.n_nd && P.p < P.nsz) atomicOr(&BM[P.p >> 5], 1u << (P.p & 31));
+    wave_sync();
+    const uint32_t klo = (uint32_t)P.nkey, khi = (uint32_t)(P.nkey >> 32);
+    for (int b_hi = nch; b_hi > 0; b_hi -= kBatch) {
+      const int b_lo = max(0, b_hi - kBatch);
+      const uint32_t wv = lane < 2 * (b_hi - b_lo) ? BM[w_lo + 2 * b_lo + lane] : 0u;
+      uint64_t val[kBatch];
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        val[t] = 0;
+        if (b_lo + t < b_hi) {
+          const int ob = ob_lo + kWave * (b_lo + t);
+          uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * t + 1) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * t);
+          const int valid = P.nsz - ob;
+          if (valid < kWave) mo &= (1ull << valid) - 1;
+          const int nb = __popcll(ballot64(lane < P.n_nd && P.p < ob)) + rank_below(mo);
+          const bool isnew = (mo >> lane) & 1;
+          const int src = nb & (kWave - 1);
+          const uint32_t nlo = (uint32_t)__shfl((int)klo, src, kWave);
+          const uint32_t nhi = (uint32_t)__shfl((int)khi, src, kWave);
+          const int j = ob + lane;
+          uint64_t ov = 0;
+          if (!isnew && j < P.nsz) ov = A[j - nb];
+          val[t] = isnew ? (((uint64_t)nhi << 32) | nlo) : ov;
+        }
+      }
       wave_sync();
-      if (ins && P.r >= base && P.r < base + kWave) atomicAdd(&H[P.r - base], 1);
-      const int c0 = __popcll(ballot64(ins && P.r < base));
-      wave_sync();
-      const int d = i + c0 + wave_incl_scan(H[lane]);
-      wave_sync();
-      if (i < sz && d < L && d != i) A[d] = v;
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        const int j = ob_lo + kWave * (b_lo + t) + lane;
+        if (b_lo + t < b_hi && j < P.nsz) A[j] = val[t];
+      }
       wave_sync();
     }
-    if (ins && P.p < L) A[P.p] = P.nkey;
-    wave_sync();
   }
   if (P.cand < 0) return P.nsz;
-  if (lane == 0) A[P.cand] = P.sel | kVisited;
+  if (lane == 0) A[P.cand] = P.sel | kListVisited;
   wave_sync();
   int nfu = P.nsz;
   for (int base = P.cand + 1; base < P.nsz; base += kWave) {
     const int i = base + lane;
-    const uint64_t m = ballot64(i < P.nsz && !(entry_id(A[i]) & kVisited));
+    const uint64_t m = ballot64(i < P.nsz && !entry_visited(A[i]));
     if (m) {
       nfu = base + (int)__builtin_ctzll(m);
       break;
@@ -371,6 +413,62 @@ __device__ __forceinline__ void topk_push(float* td, int32_t* ti, int* found, in
   wave_sync();
 }
 
+// The same insertion with the list in registers (k <= 64): lane j holds
+// element j and the shift is one DPP lane shift.
+__device__ __forceinline__ void topk_push_regs(float& td, int32_t& ti, int& found, int k, float d,
+                                               int32_t id) {
+  const int lane = lane_id();
+  const int n = found;
+  const uint64_t ng = ballot64(lane < n && !(td > d));
+  const int pos = ng ? 64 - (int)__builtin_clzll(ng) : 0;
+  const int last = min(n, k - 1);
+  const float sd = __uint_as_float(lane_shr1(__float_as_uint(td)));
+  const int32_t si = (int32_t)lane_shr1((uint32_t)ti);
+  if (lane > pos && lane <= last) {
+    td = sd;
+    ti = si;
+  }
+  if (lane == pos && pos < k) {
+    td = d;
+    ti = id;
+  }
+  if (n + 1 <= k) found = n + 1;
+}
+
+// Top-k state of one query: registers for k <= 64, else the LDS arrays td/ti.
+struct TopK {
+  float* td;
+  int32_t* ti;
+  int k, found;
+  float rd;
+  int32_t ri;
+  __device__ __forceinline__ TopK(float* td_, int32_t* ti_, int k_)
+      : td(td_), ti(ti_), k(k_), found(0), rd(0.0f), ri(0) {}
+  __device__ __forceinline__ void push(float d, int32_t id) {
+    if (k <= kWave)
+      topk_push_regs(rd, ri, found, k, d, id);
+    else
+      topk_push(td, ti, &found, k, d, id);
+  }
+  // slots past found are 0, as in the reference's zero-initialised vectors
+  __device__ __forceinline__ void store(int32_t* nns, float* dists, int64_t qi) const {
+    const int lane = lane_id();
+    if (k <= kWave) {
+      if (lane < k) {
+        const bool ok = lane < found;
+        nns[qi * k + lane] = ok ? ri : 0;
+        dists[qi * k + lane] = ok ? rd : 0.0f;
+      }
+    } else {
+      for (int j = lane; j < k; j += kWave) {
+        const bool ok = j < found;
+        nns[qi * k + j] = ok ? ti[j] : 0;
+        dists[qi * k + j] = ok ? td[j] : 0.0f;
+      }
+    }
+  }
+};
+
 __device__ __forceinline__ const uint8_t* record_of(const IndexDev& ix, int64_t u) {
   return ix.pages + (u / ix.nodes_per_page) * 4096 + (u % ix.nodes_per_page) * ix.node_len;
 }
@@ -412,19 +510,17 @@ struct RecRegs {
         acc = fma_f(d, d, acc);
       }
     }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 32);
-    return __shfl(acc, 0, kWave);
+    return square_sum_tree(acc);
   }
 };
 
-// LDS carve-up of the fused kernel (bytes): LUT | qr | list A (L) | NR (64
-// ints) | top-k dists | top-k ids.
+// LDS carve-up of the fused kernel (bytes): LUT | qr | list A (L) | list
+// scratch | top-k dists | top-k ids.
 struct SearchSmem {
   static __host__ __device__ size_t bytes(int M, int dim, int L, int R, int k) {
     (void)R;
-    return (size_t)M * kPivots * 4 + (size_t)((dim + 1) & ~1) * 4 + (size_t)L * 8 + kWave * 4 +
-           (size_t)k * 8;
+    return (size_t)M * kPivots * 4 + (size_t)((dim + 1) & ~1) * 4 + (size_t)L * 8 +
+           (size_t)list_scratch_words(L) * 4 + (size_t)k * 8;
   }
 };
 
@@ -464,8 +560,8 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   float* lut = reinterpret_cast<float*>(smem_raw);
   float* qr = lut + M * kPivots;
   uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
-  int32_t* NR = reinterpret_cast<int32_t*>(A + L);
-  float* td = reinterpret_cast<float*>(NR + kWave);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
 
   int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
@@ -482,7 +578,8 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   lut_build<W>(pq, qr, lut, lane, kWave);
   __syncthreads();
 
-  int sz = 0, fu = 0, found = 0;
+  int sz = 0, fu = 0;
+  TopK top(td, ti, topk);
   int32_t exps = 0, adcs = 0;
   const int64_t cap = ix.num_pts + 2;
   while (u >= 0 && exps < cap) {
@@ -498,26 +595,20 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
     }
     // exact rerank of u (independent of the list update; :420-423)
     const float du = cur.l2(qv, dim);
-    key = wave_sort64(key);
     const ListPlan P = list_plan(A, L, key, deg, sz, fu);
     const int32_t next =
-        __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1);
+        __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)entry_id(P.sel) : -1);
     RecRegs<T, kMaxDimRegs> nxt;
     if (next >= 0) nxt.load(ix, next);
-    fu = list_apply(A, NR, L, sz, P);
+    fu = list_apply(A, BM, P);
     sz = P.nsz;
-    topk_push(td, ti, &found, topk, du, u);
+    top.push(du, u);
     u = next;
     cur = nxt;
   }
-  // results; slots past found stay 0 as in the reference's zero-initialised vectors
-  for (int j = lane; j < topk; j += kWave) {
-    const bool ok = j < found;
-    nns[(int64_t)qi * topk + j] = ok ? ti[j] : 0;
-    dists[(int64_t)qi * topk + j] = ok ? td[j] : 0.0f;
-  }
+  top.store(nns, dists, qi);
   if (lane == 0) {
-    found_cnt[qi] = found;
+    found_cnt[qi] = top.found;
     if (n_exp) n_exp[qi] = exps;
     if (n_adc) n_adc[qi] = adcs;
   }
@@ -534,27 +625,25 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
 // (src/impl/pure_mem.cuh:306-308), so the distances are bit-identical to the
 // LUT path while a query needs only its list, query vector and top-k in LDS.
 //
-// Pivot rows are stored with their 16-byte groups permuted by
-// g -> g ^ (c & gmask) so the lanes of a wave, which read random rows at
-// the same chunk, spread over the LDS banks.
+// Pivot row c (the dim floats of code c) starts at byte c*4*dim + (c & 0xF0):
+// each run of 16 rows sits 16 bytes further than the previous one, which
+// spreads the lanes of a wave (random rows, same chunk) over the LDS banks
+// for 240 bytes of padding, and a chunk's offset inside its row stays a
+// compile-time immediate of the LDS read.
 
 struct CbSmem {
-  // per-wave bytes: list (L) | 64-int scratch | top-k d | top-k id
+  // per-wave bytes: list (L) | list scratch | top-k d, top-k id (LDS only
+  // when k > 64; smaller top-k lists live in registers)
   static __host__ __device__ size_t wave_bytes(int dim, int L, int k) {
     (void)dim;
-    size_t b = (size_t)L * 8 + kWave * 4 + (size_t)k * 8;
+    size_t b = (size_t)L * 8 + (size_t)list_scratch_words(L) * 4 + (k > kWave ? (size_t)k * 8 : 0);
     return (b + 15) & ~(size_t)15;
   }
-  static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * dim * 4; }
+  static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * dim * 4 + 240; }
 };
 
-__host__ __device__ inline int cb_gmask(int dim) {
-  const int groups = dim / 4;
-  if (dim % 4 != 0) return 0;
-  if (groups % 16 == 0) return 15;
-  if (groups % 8 == 0) return 7;
-  if (groups % 4 == 0) return 3;
-  return 0;
+__device__ __forceinline__ uint32_t cb_row(uint32_t c, uint32_t rowb) {
+  return __umul24(c, rowb) + (c & 0xF0u);
 }
 
 // q - mu of every query (src/impl/pq.cuh:22-24), read back with uniform
@@ -565,51 +654,82 @@ __global__ void query_centre_kernel(const float* __restrict__ q, const float* __
   if (i < n) qs[i] = q[i] - centroid[i % dim];
 }
 
-// Float index of element i of pivot row c in the swizzled LDS table.
-__device__ __forceinline__ int cb_index(int c, int i, int dim, int gmask) {
-  return c * dim + ((((i >> 2) ^ (c & gmask)) << 2) | (i & 3));
+// Chunk distance of pivot vector p against q - mu, accumulated over the
+// chunk's dims in ascending order from 0 as the LUT build does.
+template <int W>
+__device__ __forceinline__ float cb_chunk(const float* qc, const float* p) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    const float d = qc[i] - p[i];
+    acc = fma_f(d, d, acc);
+  }
+  return acc;
 }
 
+template <int W>
+struct PivotVec;
+template <>
+struct PivotVec<4> {
+  typedef float __attribute__((ext_vector_type(4))) type;
+};
+template <>
+struct PivotVec<2> {
+  typedef float __attribute__((ext_vector_type(2))) type;
+};
+
+// ADC distance of one code row from the pivots in LDS (piv: byte base of the
+// table, rowb = 4*dim).  The pivot reads of 8 chunks are issued together;
+// q - mu is read 8 chunks at a time with uniform loads from qs, whose
+// address is made opaque per group so the compiler does not keep all of it
+// in scalar registers across expansions.
 template <int W, int MW>
-__device__ __forceinline__ float cb_adc(const float* piv, const float* qs, int dim, int gmask,
+__device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uint32_t rowb,
                                         const PQDev& pq, const CodeRow<MW>& row,
                                         const uint8_t* crow) {
   float dist = 0.0f;
-  const int M = pq.M;
-  auto chunk = [&](int m, uint32_t c) -> float {
-    float acc = 0.0f;
-    if constexpr (W == 4) {
-      const float4 p = *reinterpret_cast<const float4*>(piv + cb_index((int)c, 4 * m, dim, gmask));
-      const float4 qv = *reinterpret_cast<const float4*>(qs + 4 * m);
-      float d;
-      d = qv.x - p.x; acc = fma_f(d, d, acc);
-      d = qv.y - p.y; acc = fma_f(d, d, acc);
-      d = qv.z - p.z; acc = fma_f(d, d, acc);
-      d = qv.w - p.w; acc = fma_f(d, d, acc);
-    } else if constexpr (W == 2) {
-      const float2 p = *reinterpret_cast<const float2*>(piv + cb_index((int)c, 2 * m, dim, gmask));
-      const float2 qv = *reinterpret_cast<const float2*>(qs + 2 * m);
-      float d;
-      d = qv.x - p.x; acc = fma_f(d, d, acc);
-      d = qv.y - p.y; acc = fma_f(d, d, acc);
-    } else {
-      const int lo = pq.chunk_off[m], hi = pq.chunk_off[m + 1];
-      for (int i = lo; i < hi; ++i) {
-        const float d = qs[i] - piv[cb_index((int)c, i, dim, gmask)];
-        acc = fma_f(d, d, acc);
-      }
-    }
-    return acc;
-  };
-  if constexpr (MW > 0) {
+  if constexpr (MW > 0 && (W == 4 || W == 2)) {
+    typedef typename PivotVec<W>::type PV;
 #pragma unroll
     for (int k = 0; k < MW; ++k) {
       const uint32_t ws[4] = {row.w[k].x, row.w[k].y, row.w[k].z, row.w[k].w};
 #pragma unroll
-      for (int b = 0; b < 16; ++b) dist = dist + chunk(k * 16 + b, (ws[b >> 2] >> (8 * (b & 3))) & 0xffu);
+      for (int h = 0; h < 2; ++h) {
+        PV p[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const int bb = 8 * h + b;
+          const uint32_t c = (ws[bb >> 2] >> (8 * (bb & 3))) & 0xffu;
+          p[b] = *reinterpret_cast<const PV*>(piv + cb_row(c, rowb) + (16 * k + bb) * W * 4);
+        }
+        // uniform address in the constant address space: scalar loads
+        uint64_t qa = (uint64_t)(qs + (16 * k + 8 * h) * W);
+        asm volatile("" : "+s"(qa));
+        const __attribute__((address_space(4))) float* qg =
+            (const __attribute__((address_space(4))) float*)qa;
+        float qv[8 * W];
+#pragma unroll
+        for (int i = 0; i < 8 * W; ++i) qv[i] = qg[i];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          float pv[W];
+#pragma unroll
+          for (int i = 0; i < W; ++i) pv[i] = p[b][i];
+          dist = dist + cb_chunk<W>(qv + b * W, pv);
+        }
+      }
     }
   } else {
-    for (int m = 0; m < M; ++m) dist = dist + chunk(m, crow[m]);
+    const float* pf = reinterpret_cast<const float*>(piv);
+    for (int m = 0; m < pq.M; ++m) {
+      const uint32_t base = cb_row(crow[m], rowb) / 4;
+      float acc = 0.0f;
+      for (int i = pq.chunk_off[m]; i < pq.chunk_off[m + 1]; ++i) {
+        const float d = qs[i] - pf[base + i];
+        acc = fma_f(d, d, acc);
+      }
+      dist = dist + acc;
+    }
   }
   return dist;
 }
@@ -627,12 +747,12 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
                                                          const float* __restrict__ qs_all) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
-  const int gmask = cb_gmask(dim);
-  float* piv = reinterpret_cast<float*>(smem_raw);
-  // pivot table, swizzled (whole workgroup), the only workgroup barrier
+  const uint32_t rowb = 4u * (uint32_t)dim;
+  const uint8_t* piv = smem_raw;
+  // pivot table (whole workgroup), the only workgroup barrier
   for (int idx = threadIdx.x; idx < kPivots * dim; idx += blockDim.x) {
     const int c = idx / dim, i = idx - c * dim;
-    piv[cb_index(c, i, dim, gmask)] = pq.pivots[idx];
+    *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, rowb) + 4 * i) = pq.pivots[idx];
   }
   __syncthreads();
 
@@ -640,8 +760,8 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
   const int wave = threadIdx.x >> 6;
   uint8_t* wbase = smem_raw + CbSmem::pivot_bytes(dim) + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
   uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
-  int32_t* NR = reinterpret_cast<int32_t*>(A + L);
-  float* td = reinterpret_cast<float*>(NR + kWave);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
   const int64_t cap = ix.num_pts + 2;
 
@@ -656,7 +776,8 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
     const float* qs = qs_all + (int64_t)qi * dim;  // q - mu, uniform reads
     float qv[kMaxDimRegs];
     restored_query_regs(q + (int64_t)qi * dim, pq.centroid, dim, qv);
-    int sz = 0, fu = 0, found = 0;
+    int sz = 0, fu = 0;
+    TopK top(td, ti, topk);
     int32_t exps = 0, adcs = 0;
     while (u >= 0 && exps < cap) {
       ++exps;
@@ -667,28 +788,23 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
         CodeRow<MW> row;
         const uint8_t* crow = pq.codes + (int64_t)cur.v * M;
         row.load(crow, M);
-        key = make_key(cb_adc<W, MW>(piv, qs, dim, gmask, pq, row, crow), cur.v);
+        key = make_key(cb_adc<W, MW>(piv, qs, rowb, pq, row, crow), cur.v);
       }
       const float du = cur.l2(qv, dim);
-      key = wave_sort64(key);
       const ListPlan P = list_plan(A, L, key, deg, sz, fu);
       const int32_t next =
-          __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1);
+          __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)entry_id(P.sel) : -1);
       RecRegs<T, kMaxDimRegs> nxt;
       if (next >= 0) nxt.load(ix, next);
-      fu = list_apply(A, NR, L, sz, P);
+      fu = list_apply(A, BM, P);
       sz = P.nsz;
-      topk_push(td, ti, &found, topk, du, u);
+      top.push(du, u);
       u = next;
       cur = nxt;
     }
-    for (int j = lane; j < topk; j += kWave) {
-      const bool ok = j < found;
-      nns[(int64_t)qi * topk + j] = ok ? ti[j] : 0;
-      dists[(int64_t)qi * topk + j] = ok ? td[j] : 0.0f;
-    }
+    top.store(nns, dists, qi);
     if (lane == 0) {
-      found_cnt[qi] = found;
+      found_cnt[qi] = top.found;
       if (n_exp) n_exp[qi] = exps;
       if (n_adc) n_adc[qi] = adcs;
     }
@@ -748,8 +864,8 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
   const int dim = ix.dim, M = pq.M, R = ix.R;
   float* qr = reinterpret_cast<float*>(smem_raw);
   uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
-  int32_t* NR = reinterpret_cast<int32_t*>(A + L);
-  float* td = reinterpret_cast<float*>(NR + kWave);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
   const float* lut = luts + (int64_t)qi * M * kPivots;
   uint64_t* glist = lists + (int64_t)qi * L;
@@ -775,10 +891,9 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
     key = make_key(row.adc(lut, crow, M), cur.v);
   }
   const float du = cur.l2(qv, dim);
-  key = wave_sort64(key);
   const ListPlan P = list_plan(A, L, key, deg, s.sz, s.fu);
-  const int32_t next = P.cand >= 0 ? (int32_t)(entry_id(P.sel) & kMask31) : -1;
-  const int fu = list_apply(A, NR, L, s.sz, P);
+  const int32_t next = P.cand >= 0 ? (int32_t)entry_id(P.sel) : -1;
+  const int fu = list_apply(A, BM, P);
   const int sz = P.nsz;
   int found = s.found;
   topk_push(td, ti, &found, topk, du, u);
@@ -916,7 +1031,8 @@ template <typename T>
 hipError_t launch_round_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
                           const float* luts, int topk, int L, uint64_t* lists, StepState* st,
                           int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
-  const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + (size_t)L * 8 + kWave * 4 + (size_t)topk * 8;
+  const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + (size_t)L * 8 +
+                      (size_t)list_scratch_words(L) * 4 + (size_t)topk * 8;
   return with_mw(pq.M, [&](auto mw) {
     hipLaunchKernelGGL((step_round_kernel<T, decltype(mw)::value>), dim3(nq), dim3(64), smem,
                        stream, ix, pq, q, nq, luts, topk, L, lists, st, nns, dists, active);
