@@ -235,20 +235,26 @@ __global__ __launch_bounds__(64) void nav_entry_kernel(NavDev nav, int64_t medoi
 __host__ __device__ constexpr int list_scratch_words(int L) { return 2 * ((L + kWave - 1) / kWave); }
 
 // Rank of `key` in the sorted list A[0..sz): the number of entries ordered
-// below it.  Each level splits [lo, hi) into 9 segments of s entries and
-// reads the last entry of the first 8 at once; the entries below key form a
-// prefix of those probes, so their count fixes the segment holding the
-// answer.  A 512-entry list takes three dependent LDS reads.
+// below it.  A first level shared by all lanes splits the list into 9
+// segments of s entries and reads the last entry of the first 8 (uniform
+// addresses); the entries below key are a prefix of those probes, so their
+// count fixes the lane's segment, which a branchless binary search with
+// uniform steps finishes.
 __device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key, bool active) {
-  int lo = 0, hi = active ? sz : 0;
-  while (lo < hi) {
-    const int s = (hi - lo + 8) / 9;
+  if (!active) return 0;
+  int lo = 0, end = sz, span = sz;  // answer in [lo, end]; span bounds end - lo
+  if (sz > 8) {
+    const int s = (sz + 8) / 9;
     int cnt = 0;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) cnt += A[min(lo + s * (m + 1) - 1, hi - 1)] < key ? 1 : 0;
-    const int nhi = cnt == 8 ? hi : min(lo + s * (cnt + 1) - 1, hi - 1);
-    lo = min(lo + s * cnt, hi);
-    hi = nhi;
+    for (int m = 0; m < 8; ++m) cnt += A[min(s * (m + 1) - 1, sz - 1)] < key ? 1 : 0;
+    lo = min(s * cnt, sz);
+    end = cnt == 8 ? sz : min(s * (cnt + 1) - 1, sz - 1);
+    span = s;
+  }
+  for (int step = span > 0 ? 1 << (31 - __builtin_clz((unsigned)span)) : 0; step > 0; step >>= 1) {
+    const int p = lo + step - 1;
+    if (p < end && A[p] < key) lo += step;
   }
   return lo;
 }
