@@ -158,10 +158,13 @@ def bench_adc(args):
 def bench_search(args):
     import torch
     from gustann_amd import index as gi
-    from gustann_amd.search import GustANN, GustANNConfig, UINT8
+    from gustann_amd.search import FLOAT, GustANN, GustANNConfig, UINT8
 
-    spec = gi.DatasetSpec(name=f"mix{args.n}", n=args.n, dim=128, nclusters=args.nclusters, R=64,
-                          L_build=100, M=32, nq=args.nq_search, k=10, nav_n=args.nav_n,
+    u8 = args.dtype == "uint8"
+    sigma = args.sigma if args.sigma > 0 else (12.0 if u8 else 0.05)
+    spec = gi.DatasetSpec(name=f"mix{args.n}x{args.dim}{'' if u8 else 'f'}", n=args.n, dim=args.dim,
+                          dtype=args.dtype, nclusters=args.nclusters, sigma=sigma, R=64,
+                          L_build=100, M=args.M, nq=args.nq_search, k=10, nav_n=args.nav_n,
                           gt_nq=args.gt_nq)
     out_dir = args.data_dir or os.path.join("/tmp", f"gann_{spec.name}_{args.nav_n}")
     meta_path = os.path.join(out_dir, "meta.json")
@@ -171,10 +174,11 @@ def bench_search(args):
         log(f"[bench] building {spec.name} under {out_dir}")
         meta = gi.build_dataset(spec, out_dir, verbose=True)
     P = meta["paths"]
-    Q = gi.read_vecs(P["query"], np.uint8).astype(np.float32)
+    Q = gi.read_vecs(P["query"], np.uint8 if u8 else np.float32).astype(np.float32)
     gt = gi.read_vecs(P["gt"], np.int32)
-    g = GustANN(UINT8)
-    g.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), True)
+    g = GustANN(UINT8 if u8 else FLOAT)
+    g.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), args.placement == "hbm")
+    D, M, s_el = args.dim, args.M, (1 if u8 else 4)
     dev = torch.device("cuda:0")
     rep = args.repeat
     Qr = np.tile(Q, (rep, 1))
@@ -206,7 +210,7 @@ def bench_search(args):
         rec = recall_at_k(res, gt, 10)
         exps = int(ne.sum().item())
         adcs = int(na.sum().item())
-        alg = exps * (128 + 4) + adcs * (4 + 32) + nq * (4 * 128 + 80)
+        alg = exps * (D * s_el + 4) + adcs * (4 + M) + nq * (4 * D + 80)
         rows.append({"L": L, "ms": ms, "qps": nq / (ms / 1e3), "recall": rec,
                      "expansions_per_query": exps / nq, "alg_GBps": alg / (ms / 1e3) / 1e9})
         log(f"[bench] L={L} {ms:.3f} ms qps={nq / (ms / 1e3):.0f} recall@10={rec:.4f}")
@@ -215,10 +219,13 @@ def bench_search(args):
     result = {
         "metric": METRIC, "value": best["qps"], "unit": "queries/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": best["ms"],
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8/f32",
-        "data": "synthetic uint8 Gaussian mixture",
-        "config": {"workload": f"in_memory_search_{args.n}x128_u8", "nq": nq, "L": best["L"],
-                   "L_sweep": rows},
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8/f32" if u8 else "f32",
+        "data": ("synthetic uint8 Gaussian mixture" if u8 else
+                 f"synthetic L2-normalised f32 Gaussian mixture (sigma {sigma})"),
+        "config": {"workload": (f"in_memory_search_{args.n}x{D}_{'u8' if u8 else 'f32'}_M{M}"
+                                + ("" if args.placement == "hbm" else "_host_pinned")),
+                   "nq": nq, "L": best["L"], "L_sweep": rows},
         "roofline": {"bound": "hbm", "achieved": best["alg_GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": best["alg_GBps"] / HBM_PEAK_GBS, "traffic": None},
     }
@@ -226,7 +233,7 @@ def bench_search(args):
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as orc
         log(f"[bench] CPU baseline (oracle beam search) at L={best['L']}")
-        ix = orc.Index(P["index"], P["pq"], P["nav"])
+        ix = orc.Index(P["index"], P["pq"], P["nav"], dtype=args.dtype)
         threads = min(16, os.cpu_count() or 1)
         n0 = min(256, Q.shape[0])
         t = time.perf_counter()
@@ -240,7 +247,7 @@ def bench_search(args):
                                   "kind": "port",
                                   "sample": f"first {n} queries at L={best['L']}: oracle/gann_oracle.c "
                                             f"orc_search, {threads} threads, {dt:.1f} s"}
-        g2 = GustANN(UINT8)
+        g2 = GustANN(UINT8 if u8 else FLOAT)
         g2.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), True)
         gn, gd, gf = g2.search(Q[:n], n, 10, best["L"])
         g2.close()
@@ -291,6 +298,11 @@ def main():
     ap.add_argument("--repeat", type=int, default=1)
     ap.add_argument("--L", type=int, nargs="+", default=[32, 48, 64, 96, 128])
     ap.add_argument("--data-dir", default="")
+    ap.add_argument("--dtype", choices=["uint8", "float"], default="uint8")
+    ap.add_argument("--dim", type=int, default=128)
+    ap.add_argument("--M", type=int, default=32)
+    ap.add_argument("--sigma", type=float, default=0.0, help="0 = 12 (uint8) / 0.05 (float)")
+    ap.add_argument("--placement", choices=["hbm", "pinned"], default="hbm")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (queries shard across "

@@ -18,7 +18,7 @@ MODE_FUSED, MODE_STEPWISE, MODE_FUSED_LUT = 0, 1, 2
 # Every symbol declared in include/gustann.h.
 ABI_SYMBOLS = (
     "gann_last_error", "gann_version", "gann_open", "gann_close", "gann_get_info",
-    "gann_search", "gann_search_ex", "gann_search_device", "gann_nav_entry",
+    "gann_search", "gann_search_ex", "gann_search_device", "gann_search_device_ex", "gann_nav_entry",
     "gann_pq_open", "gann_pq_create", "gann_pq_close", "gann_handle_pq",
     "gann_pq_lut_build", "gann_pq_adc_scan", "gann_pq_adc_scan_device",
 )
@@ -62,6 +62,8 @@ _SIGS = {
     "gann_search_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P,
                                  C.POINTER(Stats)]),
     "gann_search_device": (C.c_int, [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P]),
+    "gann_search_device_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P,
+                                        _P, _P]),
     "gann_nav_entry": (C.c_int, [_P, _P, _I32, _P, _P]),
     "gann_pq_open": (C.c_int, [C.c_char_p, _I32, C.POINTER(_P)]),
     "gann_pq_create": (C.c_int, [_P, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, C.POINTER(_P)]),
@@ -122,6 +124,7 @@ def check(rc: int):
 
 _IDX_SIGS = {
     "gib_last_error": (C.c_char_p, []),
+    "gib_set_verbose": (None, [C.c_int]),
     "gib_gen_mixture_u8": (C.c_int, [_I64, _I64, _I64, C.c_uint64, C.c_uint64, C.c_double,
                                      C.c_double, C.c_double, _P, _P, _P, C.c_int]),
     "gib_gen_mixture_f32": (C.c_int, [_I64, _I64, _I64, C.c_uint64, C.c_uint64, C.c_double, _P,

@@ -4,6 +4,7 @@ Products:
   gustann_amd/lib/libgustann_hip.so    HIP kernels (gfx950) + C ABI (include/gustann.h)
   gustann_amd/lib/libgustann_index.so  host C++ index builder / data generator
   gustann_amd/lib/search_mem           search_mem-compatible command line
+  gustann_amd/lib/check_recall         check_recall-compatible command line
   oracle/liboracle_gann.so             CPU oracle (test infrastructure; built by oracle/Makefile)
 
 Run ``python -m gustann_amd.build`` or call :func:`build_all`.
@@ -82,6 +83,14 @@ def build_cli(verbose=False):
     return out
 
 
+def build_check_recall(verbose=False):
+    out = os.path.join(LIB, "check_recall")
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-o", out + ".tmp", os.path.join(CSRC, "check_recall.cpp"),
+          f"-I{CSRC}"], verbose)
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_oracle(verbose=False):
     odir = os.path.join(ROOT, "oracle")
     _run(["make", "-s", "-C", odir, "-B", "liboracle_gann.so"], verbose)
@@ -91,7 +100,8 @@ def build_oracle(verbose=False):
 def build_all(verbose=False):
     if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    paths = [build_hip(verbose), build_index(verbose), build_oracle(verbose)]
+    paths = [build_hip(verbose), build_index(verbose), build_oracle(verbose),
+             build_check_recall(verbose)]
     cli = build_cli(verbose)
     if cli:
         paths.append(cli)

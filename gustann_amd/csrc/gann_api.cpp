@@ -384,7 +384,9 @@ void validate_search(const gann_handle* h, int32_t nq, int32_t topk, int32_t L, 
   if (nq < 0) raise(GANN_ERR_INVALID, "nq must be >= 0");
   if (topk < 1) raise(GANN_ERR_INVALID, "topk must be >= 1");
   if (L < topk) raise(GANN_ERR_INVALID, "L (ef_search) must be >= topk (bin/search_disk.cpp:189-192)");
-  if (beam != 1) raise(GANN_ERR_UNSUPPORTED, "beam_width must be 1 (one node per iteration)");
+  if (beam < 1 || beam > gann::max_beam_width())
+    raise(GANN_ERR_UNSUPPORTED, "beam_width must be in [1, " + std::to_string(gann::max_beam_width()) +
+                                    "] (1 = the reference's one node per iteration)");
   if (h->layout.max_m > 64)
     raise(GANN_ERR_UNSUPPORTED, "graph degree R > 64 is not supported by the wave64 kernels");
   if (h->layout.dim > 256)
@@ -408,8 +410,23 @@ void run_entries(gann_handle* h, const float* q_dev, int32_t nq, int32_t* entrie
 
 void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                 int32_t mode, const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
-                int32_t* nexp, int32_t* nadc, hipStream_t s) {
+                int32_t* nexp, int32_t* nadc, hipStream_t s, int32_t beam = 1) {
   const gann::DiskLayout& Ly = h->layout;
+  if (beam > 1) {
+    // beam search: shared-codebook kernel only
+    if (mode != GANN_MODE_FUSED)
+      raise(GANN_ERR_UNSUPPORTED, "beam_width > 1 runs only in GANN_MODE_FUSED");
+    const int waves = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit);
+    if (waves < 1)
+      raise(GANN_ERR_UNSUPPORTED, "beam_width > 1 needs the pivot table and one list in LDS");
+    h->counters.ensure(64);
+    h->qs.ensure((size_t)nq * Ly.dim * 4);
+    const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
+    GANN_HIP(gann::launch_search_beam(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, beam,
+                                      nns, dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
+                                      h->qs.as<float>(), waves, blocks, s));
+    return;
+  }
   if (mode == GANN_MODE_FUSED) {
     // one workgroup per CU holding the pivot table, as many waves as fit
     const int waves = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit);
@@ -540,7 +557,7 @@ int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int
     const double t1 = now_s();
     run_search(h, h->q.as<float>(), nq, topk, L, mode, h->entries.as<int32_t>(), h->nns.as<int32_t>(),
                h->dists.as<float>(), h->found.as<int32_t>(), h->nexp.as<int32_t>(),
-               h->nadc.as<int32_t>(), s);
+               h->nadc.as<int32_t>(), s, beam_width);
     GANN_HIP(hipStreamSynchronize(s));
     const double t2 = now_s();
     GANN_HIP(hipMemcpyAsync(nns, h->nns.p, (size_t)nq * topk * 4, hipMemcpyDeviceToHost, s));
@@ -578,12 +595,13 @@ int gann_search(gann_handle* h, const float* q, int32_t nq, int32_t topk, int32_
                         nullptr, st);
 }
 
-int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
-                       int32_t* entries_dev, int32_t* nns_dev, float* dists_dev,
-                       int32_t* found_dev, int32_t* n_exp_dev, int32_t* n_adc_dev, void* stream) {
+int gann_search_device_ex(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                          int32_t beam_width, int32_t mode, int32_t* entries_dev, int32_t* nns_dev,
+                          float* dists_dev, int32_t* found_dev, int32_t* n_exp_dev,
+                          int32_t* n_adc_dev, void* stream) {
   return guarded([&] {
     if (!h) raise(GANN_ERR_INVALID, "handle is NULL");
-    validate_search(h, nq, topk, L, 1);
+    validate_search(h, nq, topk, L, beam_width);
     if (nq == 0) return;
     if (!q_dev || !entries_dev || !nns_dev || !dists_dev || !found_dev)
       raise(GANN_ERR_INVALID, "NULL buffer");
@@ -591,9 +609,16 @@ int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t t
     hipStream_t s = (hipStream_t)stream;
     h->counters.ensure(64);
     run_entries(h, q_dev, nq, entries_dev, nullptr, h->counters.as<int32_t>(), s);
-    run_search(h, q_dev, nq, topk, L, GANN_MODE_FUSED, entries_dev, nns_dev, dists_dev, found_dev,
-               n_exp_dev, n_adc_dev, s);
+    run_search(h, q_dev, nq, topk, L, mode, entries_dev, nns_dev, dists_dev, found_dev, n_exp_dev,
+               n_adc_dev, s, beam_width);
   });
+}
+
+int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                       int32_t* entries_dev, int32_t* nns_dev, float* dists_dev,
+                       int32_t* found_dev, int32_t* n_exp_dev, int32_t* n_adc_dev, void* stream) {
+  return gann_search_device_ex(h, q_dev, nq, topk, L, 1, GANN_MODE_FUSED, entries_dev, nns_dev,
+                               dists_dev, found_dev, n_exp_dev, n_adc_dev, stream);
 }
 
 int gann_nav_entry(gann_handle* h, const float* q, int32_t nq, int32_t* entries_out,

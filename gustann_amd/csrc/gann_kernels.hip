@@ -273,6 +273,7 @@ struct ListPlan {
   int cand;       // position of the next node in the new list (uniform, -1: stop)
   uint64_t sel;   // the selected entry (uniform)
   int nsz;        // new list size (uniform)
+  int lb;         // every entry before lb is visited in the new list (uniform, <= nsz)
 };
 
 // Ranks each lane's candidate (lanes < deg) in the list, drops those whose id
@@ -297,6 +298,7 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
   int fu_new = INT_MAX;
   if (fu < sz) fu_new = fu + __popcll(ballot64(lane < P.n_nd && (int)r <= fu));
   const int cand = min(fu_new, P.p0);
+  P.lb = min(cand, P.nsz);
   if (cand >= P.nsz) {
     P.cand = -1;
     P.sel = 0;
@@ -314,6 +316,8 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
 // batches of 8 chunks, top batch first: a batch reads only positions at or
 // above its lowest output minus 64 and writes after all its reads, so no
 // source is overwritten before it is read.
+// kSelect = false (beam search) only applies the insertions and returns P.lb.
+template <bool kSelect = true>
 __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListPlan& P) {
   constexpr int kBatch = 8;
   const int lane = lane_id();
@@ -361,6 +365,7 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
       wave_sync();
     }
   }
+  if (!kSelect) return P.lb;
   if (P.cand < 0) return P.nsz;
   if (lane == 0) A[P.cand] = P.sel | kListVisited;
   wave_sync();
@@ -534,11 +539,12 @@ constexpr int kMaxDimRegs = 8;  // rerank coordinates per lane: dim <= 256
 
 // The restored query fl(fl(q - mu) + mu) (src/impl/pq.cuh:22-24, 54-56) in
 // the rerank lane roles: lane l holds dims l, l+32, ...
+template <int N>
 __device__ __forceinline__ void restored_query_regs(const float* q, const float* centroid, int dim,
-                                                    float (&qv)[kMaxDimRegs]) {
+                                                    float (&qv)[N]) {
   const int l = lane_id() & 31;
 #pragma unroll
-  for (int k = 0; k < kMaxDimRegs; ++k) {
+  for (int k = 0; k < N; ++k) {
     const int i = l + 32 * k;
     float v = 0.0f;
     if (i < dim) {
@@ -807,6 +813,136 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
       top.push(du, u);
       u = next;
       cur = nxt;
+    }
+    top.store(nns, dists, qi);
+    if (lane == 0) {
+      found_cnt[qi] = top.found;
+      if (n_exp) n_exp[qi] = exps;
+      if (n_adc) n_adc[qi] = adcs;
+    }
+    wave_sync();
+  }
+}
+
+// ------------------------------------------------------------------ beam search, beam width > 1
+
+// Beam search with beam width bw (2..kMaxBeam), a mode the reference does not
+// have (it expands one node per iteration; this mode is reported beside it
+// with its own recall).  Each round takes the first bw unvisited list entries
+// at once, marks them visited and loads their records together, then expands
+// them in list order: every expansion merges its neighbours into the list
+// with the same rank / sort / gather update as search_cb_kernel and pushes
+// the node's exact distance into the top-k.  The code rows of the next node
+// of the round are fetched while the current one is merged.  The search ends
+// when no unvisited entry is left.  LDS layout and query queue as in
+// search_cb_kernel; KP rerank coordinates per lane (dim <= 32 * KP).
+constexpr int kMaxBeam = 4;
+
+template <typename T, int MW, int W, int KP>
+__global__ __launch_bounds__(1024) void search_beam_kernel(IndexDev ix, PQDev pq,
+                                                           const float* __restrict__ q, int nq,
+                                                           const int32_t* __restrict__ entries,
+                                                           int topk, int L, int bw,
+                                                           int32_t* __restrict__ nns,
+                                                           float* __restrict__ dists,
+                                                           int32_t* __restrict__ found_cnt,
+                                                           int32_t* __restrict__ n_exp,
+                                                           int32_t* __restrict__ n_adc,
+                                                           int32_t* __restrict__ queue,
+                                                           const float* __restrict__ qs_all) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  const int dim = ix.dim, M = pq.M, R = ix.R;
+  const uint32_t rowb = 4u * (uint32_t)dim;
+  const uint8_t* piv = smem_raw;
+  for (int idx = threadIdx.x; idx < kPivots * dim; idx += blockDim.x) {
+    const int c = idx / dim, i = idx - c * dim;
+    *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, rowb) + 4 * i) = pq.pivots[idx];
+  }
+  __syncthreads();
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  uint8_t* wbase = smem_raw + CbSmem::pivot_bytes(dim) + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
+  uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
+  int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
+  const int64_t cap = ix.num_pts + 2;
+
+  for (;;) {
+    int qi = 0;
+    if (lane == 0) qi = atomicAdd(queue, 1);
+    qi = __builtin_amdgcn_readfirstlane(__shfl(qi, 0, kWave));
+    if (qi >= nq) break;
+    const float* qs = qs_all + (int64_t)qi * dim;
+    float qv[KP];
+    restored_query_regs(q + (int64_t)qi * dim, pq.centroid, dim, qv);
+    int sz = 0, fu = 0;
+    TopK top(td, ti, topk);
+    int32_t exps = 0, adcs = 0;
+    int32_t sel[kMaxBeam];
+#pragma unroll
+    for (int b = 0; b < kMaxBeam; ++b) sel[b] = -1;
+    sel[0] = __builtin_amdgcn_readfirstlane(entries[qi]);
+    int nsel = sel[0] >= 0 ? 1 : 0;
+    while (nsel > 0) {
+      RecRegs<T, KP> rec[kMaxBeam];
+#pragma unroll
+      for (int b = 0; b < kMaxBeam; ++b)
+        if (b < nsel) rec[b].load(ix, sel[b]);
+      CodeRow<MW> rows[2];
+      {
+        const int d0 = __builtin_amdgcn_readfirstlane(min(max(rec[0].deg_raw, 0), R));
+        if (lane < d0) rows[0].load(pq.codes + (int64_t)rec[0].v * M, M);
+      }
+#pragma unroll
+      for (int b = 0; b < kMaxBeam; ++b) {
+        if (b < nsel && exps < cap) {
+          ++exps;
+          const int deg = __builtin_amdgcn_readfirstlane(min(max(rec[b].deg_raw, 0), R));
+          adcs += deg;
+          if (b + 1 < kMaxBeam && b + 1 < nsel) {
+            const int dn = __builtin_amdgcn_readfirstlane(min(max(rec[b + 1].deg_raw, 0), R));
+            if (lane < dn) rows[(b + 1) & 1].load(pq.codes + (int64_t)rec[b + 1].v * M, M);
+          }
+          uint64_t key = ~(uint64_t)0;
+          if (lane < deg) {
+            const uint8_t* crow = pq.codes + (int64_t)rec[b].v * M;
+            key = make_key(cb_adc<W, MW>(piv, qs, rowb, pq, rows[b & 1], crow), rec[b].v);
+          }
+          const float du = rec[b].l2(qv, dim);
+          const ListPlan P = list_plan(A, L, key, deg, sz, fu);
+          fu = list_apply<false>(A, BM, P);
+          sz = P.nsz;
+          top.push(du, sel[b]);
+        }
+      }
+      // next round: the first bw unvisited entries at or after fu (every
+      // entry before fu is visited)
+      nsel = 0;
+      if (exps < cap) {
+        for (int base = fu; base < sz && nsel < bw; base += kWave) {
+          const int i = base + lane;
+          const uint64_t e = i < sz ? A[i] : kListVisited;
+          uint64_t m = ballot64(!entry_visited(e));
+          bool take = false;
+          int last = -1;
+          while (m != 0 && nsel < bw) {
+            const int l = (int)__builtin_ctzll(m);
+            m &= m - 1;
+            const int32_t id = (int32_t)__builtin_amdgcn_readlane((int)entry_id(e), l);
+#pragma unroll
+            for (int t = 0; t < kMaxBeam; ++t)
+              if (t == nsel) sel[t] = id;
+            take |= lane == l;
+            last = l;
+            ++nsel;
+          }
+          if (take) A[i] = e | kListVisited;
+          fu = nsel < bw ? min(base + kWave, sz) : base + last + 1;
+        }
+        wave_sync();
+      }
     }
     top.store(nns, dists, qi);
     if (lane == 0) {
@@ -1089,6 +1225,42 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
   if (dtype == 0) return go(uint8_t{});
   return go(float{});
 }
+
+hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                              const int32_t* entries, int topk, int L, int bw, int32_t* nns,
+                              float* dists, int32_t* found, int32_t* n_exp, int32_t* n_adc,
+                              int32_t* queue, float* qs_all, int waves, int blocks,
+                              hipStream_t stream) {
+  if (bw < 2 || bw > kMaxBeam) return hipErrorInvalidValue;
+  const size_t smem = CbSmem::pivot_bytes(ix.dim) + (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
+  hipError_t e = launch_fill_i32(queue, 1, 0, stream);
+  if (e != hipSuccess) return e;
+  const int64_t n = (int64_t)nq * ix.dim;
+  hipLaunchKernelGGL(query_centre_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, q,
+                     pq.centroid, n, ix.dim, qs_all);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  auto go = [&](auto t, auto kp) {
+    using T = decltype(t);
+    return with_mw(pq.M, [&](auto mw) {
+      return with_w(pq.chunk_w, [&](auto w) {
+        hipLaunchKernelGGL(
+            (search_beam_kernel<T, decltype(mw)::value, decltype(w)::value, decltype(kp)::value>),
+            dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries, topk, L, bw,
+            nns, dists, found, n_exp, n_adc, queue, qs_all);
+        return hipGetLastError();
+      });
+    });
+  };
+  const bool small = ix.dim <= 128;
+  if (dtype == 0)
+    return small ? go(uint8_t{}, std::integral_constant<int, 4>{})
+                 : go(uint8_t{}, std::integral_constant<int, kMaxDimRegs>{});
+  return small ? go(float{}, std::integral_constant<int, 4>{})
+               : go(float{}, std::integral_constant<int, kMaxDimRegs>{});
+}
+
+int max_beam_width() { return kMaxBeam; }
 
 size_t step_state_bytes() { return sizeof(StepState); }
 

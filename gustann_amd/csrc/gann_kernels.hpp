@@ -29,6 +29,14 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
                             float* qs_all, int waves, int blocks, hipStream_t stream);
+// Beam search with beam width bw in [2, max_beam_width()] (same LDS layout and
+// launch shape as launch_search_cb).
+hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
+                              const int32_t* entries, int topk, int L, int bw, int32_t* nns,
+                              float* dists, int32_t* found, int32_t* n_exp, int32_t* n_adc,
+                              int32_t* queue, float* qs_all, int waves, int blocks,
+                              hipStream_t stream);
+int max_beam_width();
 hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
                             float* luts, void* st, hipStream_t stream);
 hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,

@@ -17,6 +17,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <numeric>
@@ -29,6 +30,8 @@
 namespace {
 
 thread_local std::string g_err;
+// Progress lines on stderr during long graph builds (gib_set_verbose).
+std::atomic<int> g_verbose{0};
 
 // ------------------------------------------------------------------ RNG
 // splitmix64 seeding + xoshiro256**; Box-Muller normals.  Streams are
@@ -292,6 +295,9 @@ void vamana(const Points& P, int64_t R, int64_t L, float alpha, uint64_t seed, i
       std::vector<uint32_t> pruned, vp;
 #pragma omp for schedule(dynamic, 64)
       for (int64_t oi = 0; oi < n; ++oi) {
+        if (g_verbose.load(std::memory_order_relaxed) && n >= 1000000 && oi % (n / 20) == 0)
+          std::fprintf(stderr, "[vamana] alpha %.2f: %lld / %lld\n", (double)a, (long long)oi,
+                       (long long)n);
         int64_t p = order[(size_t)oi];
         S.search(P, G, p, (uint32_t)medoid, L);
         cand = S.pool;
@@ -461,6 +467,8 @@ void pq_encode(const Points& P, int nthreads, gann::PQHost& pq) {
 extern "C" {
 
 const char* gib_last_error(void) { return g_err.c_str(); }
+
+void gib_set_verbose(int on) { g_verbose.store(on ? 1 : 0); }
 
 // Gaussian mixture, uint8: centres ~ U[lo, hi]^dim (from centre_seed),
 // point = round(centre + N(0, sigma^2)) clipped to [0, 255] (from

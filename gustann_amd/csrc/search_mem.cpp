@@ -5,7 +5,10 @@
 //
 //   search_mem --query Q --index I --pq_data P [--nav_graph N] --data_type uint8|float
 //              [--ground_truth GT] [--topk K] --ef_search L [L ...] [-R n] [-G]
-//              [--mode fused|lut|stepwise] [--device d]
+//              [--mode fused|lut|stepwise] [--device d] [--result_path FILE]
+//
+// --result_path (an addition) writes the ids of the first L's run as a bin
+// file [nq x topk] int32, the input of check_recall.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -27,15 +30,16 @@ void check(int rc, const char* what) {
   if (rc != GANN_OK) die(std::string(what) + " failed: " + gann_last_error());
 }
 
-// calc_recall (bin/utils.hpp:104-116)
-double calc_recall(const int32_t* res, const int32_t* gt, int64_t num, int64_t dim, int k) {
+// calc_recall (bin/utils.hpp:104-116): the fraction is formed in double and
+// returned as float, which the caller prints as double.
+float calc_recall(const int32_t* res, const int32_t* gt, int64_t num, int64_t dim, int k) {
   int64_t cnt = 0;
   for (int64_t i = 0; i < num; ++i) {
     std::set<int32_t> s(gt + i * dim, gt + i * dim + k);
     for (int j = 0; j < k; ++j)
       if (s.count(res[i * k + j])) ++cnt;
   }
-  return (double)cnt / ((double)num * k);
+  return (float)(1.0 * (double)cnt / (double)(num * k));
 }
 
 void usage() {
@@ -43,13 +47,14 @@ void usage() {
                "Usage: search_mem --query FILE --index FILE --pq_data PREFIX --data_type uint8|float\n"
                "                  --ef_search L [L ...] [--ground_truth FILE] [--topk K]\n"
                "                  [--nav_graph DIR] [--repeat|-R N] [--use-gpu-mem|-G]\n"
-               "                  [--mode fused|lut|stepwise] [--device D]\n");
+               "                  [--mode fused|lut|stepwise] [--device D] [--result_path FILE]\n");
 }
 
 }  // namespace
 
 int main(int argc, char** argv) {
   std::string query_file, index_file, gt_file, data_type, pq_prefix, nav_prefix, mode_s = "fused";
+  std::string result_path;
   int topk = 100;  // bin/search_disk.cpp:29
   int repeat = 20; // :36
   int device = 0;
@@ -72,6 +77,7 @@ int main(int argc, char** argv) {
     else if (a == "--use-gpu-mem" || a == "-G") use_gpu_mem = true;
     else if (a == "--mode") mode_s = need("--mode");
     else if (a == "--device") device = std::atoi(need("--device").c_str());
+    else if (a == "--result_path") result_path = need("--result_path");
     else if (a == "--ef_search") {
       while (i + 1 < argc && argv[i + 1][0] != '-') ef.push_back(std::atoi(argv[++i]));
     } else if (a == "-h" || a == "--help") {
@@ -138,9 +144,14 @@ int main(int argc, char** argv) {
                          found.data(), nullptr, st),
           "gann_search");
   };
+  auto save = [&]() {
+    if (result_path.empty()) return;
+    if (!gann::write_bin(result_path, (int32_t)total, topk, nns.data(), 4, &err)) die(err);
+  };
   if (ef.size() == 1) {
     gann_stats st{};
     run(ef[0], &st);
+    save();
     for (int i = 0; i < 5 && i < total; ++i) {  // :199-204
       for (int j = 0; j < 5 && j < topk; ++j) std::printf("%lf(%d)\t", dis[(size_t)(i * topk + j)], nns[(size_t)(i * topk + j)]);
       std::printf("\n");
@@ -161,6 +172,7 @@ int main(int argc, char** argv) {
     for (int L : ef) {
       gann_stats st{};
       run(L, &st);
+      if (L == ef[0]) save();
       rows.push_back({L, total / st.run_time_s,
                       (have_gt && topk <= gt_d) ? calc_recall(nns.data(), gt, gt_nq, gt_d, topk) : -1});
     }

@@ -255,6 +255,7 @@ def build_dataset(spec: DatasetSpec, out_dir: str, threads=None, verbose=False) 
     import sys
     import time
     os.makedirs(out_dir, exist_ok=True)
+    index_lib().gib_set_verbose(1 if verbose else 0)
     t0 = time.time()
     s = spec.seed
     if spec.dtype == "uint8":

@@ -120,10 +120,11 @@ class GustANN:
         return ent, loc
 
     def search_device(self, q_ptr, nq, topk, L, entries_ptr, nns_ptr, dists_ptr, found_ptr,
-                      nexp_ptr=None, nadc_ptr=None, stream=None):
-        """Asynchronous fused search on device buffers (raw device pointers)."""
-        N.check(N.hip_lib().gann_search_device(self.handle, q_ptr, nq, topk, L, entries_ptr, nns_ptr,
-                                               dists_ptr, found_ptr, nexp_ptr, nadc_ptr, stream))
+                      nexp_ptr=None, nadc_ptr=None, stream=None, beam_width=1, mode=N.MODE_FUSED):
+        """Asynchronous search on device buffers (raw device pointers)."""
+        N.check(N.hip_lib().gann_search_device_ex(self.handle, q_ptr, nq, topk, L, beam_width, mode,
+                                                  entries_ptr, nns_ptr, dists_ptr, found_ptr,
+                                                  nexp_ptr, nadc_ptr, stream))
 
     def pq(self) -> "PQSearch":
         p = C.c_void_p()

@@ -92,10 +92,14 @@ int gann_open(const gann_config* cfg, gann_handle** out);
 int gann_close(gann_handle* h);
 int gann_get_info(const gann_handle* h, gann_index_info* info);
 
-/* GustANN::search.  Synchronous; q is [nq][dim] f32 row-major on the host;
- * nns/dists are [nq][topk], found_cnt [nq] on the host.  Requires
- * L >= topk (bin/search_disk.cpp:189-192).  beam_width must be 1, the
- * reference's one node per iteration.  st may be NULL. */
+/* GustANN::search (src/ssd_search.hpp:78-80, src/pure_mem.cu:71-199).
+ * Synchronous; q is [nq][dim] f32 row-major on the host; nns/dists are
+ * [nq][topk], found_cnt [nq] on the host.  Requires L >= topk
+ * (bin/search_disk.cpp:189-192).  beam_width 1 is the reference's one node
+ * per iteration (results identical to the reference); 2..4 selects the beam
+ * search of this library (the first beam_width unvisited entries are expanded
+ * per round; GANN_MODE_FUSED only), which the reference does not have.
+ * st may be NULL. */
 int gann_search(gann_handle* h, const float* q, int32_t nq, int32_t topk, int32_t L,
                 int32_t beam_width, int32_t* nns, float* dists, int32_t* found_cnt,
                 gann_stats* st);
@@ -113,6 +117,14 @@ int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int
 int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                        int32_t* entries_dev, int32_t* nns_dev, float* dists_dev,
                        int32_t* found_dev, int32_t* n_exp_dev, int32_t* n_adc_dev, void* stream);
+
+/* gann_search_device with a beam width and an execution mode (as in
+ * gann_search_ex).  No counterpart in the reference, whose search takes host
+ * arrays only; it is the device-resident form of gann_search_ex. */
+int gann_search_device_ex(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                          int32_t beam_width, int32_t mode, int32_t* entries_dev, int32_t* nns_dev,
+                          float* dists_dev, int32_t* found_dev, int32_t* n_exp_dev,
+                          int32_t* n_adc_dev, void* stream);
 
 /* get_entry_kernel + NavGraph::translate: base-graph entry per query (the
  * medoid when the handle has no pivot graph).  local_out (nullable) receives

@@ -464,6 +464,136 @@ int64_t orc_search(const orc_index* ix, const float* q, int32_t nq, const int32_
   return v;
 }
 
+/* ------------------------------------------------------------------ beam */
+
+/* orc_search_beam (gann_oracle.h): a sorted array of at most L entries. */
+typedef struct {
+  float* dist;
+  uint32_t* id;
+  uint8_t* visited;
+  int32_t size;
+} beam_list;
+
+static void beam_insert(beam_list* B, int32_t L, float d, uint32_t v) {
+  int pos = lower_bound_key(B->dist, B->id, 0, B->size, d, v);
+  for (int i = 0; i < B->size; ++i)
+    if (B->id[i] == v) return; /* listed already */
+  if (pos >= L) return;
+  int last = B->size < L ? B->size : L - 1; /* the entry at L - 1 falls off a full list */
+  for (int i = last; i > pos; --i) {
+    B->dist[i] = B->dist[i - 1];
+    B->id[i] = B->id[i - 1];
+    B->visited[i] = B->visited[i - 1];
+  }
+  B->dist[pos] = d;
+  B->id[pos] = v;
+  B->visited[pos] = 0;
+  if (B->size < L) ++B->size;
+}
+
+static void search_beam_one(const orc_index* ix, const float* q, int32_t entry, int32_t topk,
+                            int32_t L, int32_t bw, int32_t* nns, float* dists, int32_t* found,
+                            int32_t* n_exp, float* lut, float* qr, beam_list* B, int64_t* sel) {
+  const int64_t R = ix->max_m, M = ix->num_chunks;
+  const int64_t data_len = ix->dim * (ix->dtype == 0 ? 1 : 4);
+  orc_lut_build(ix->pivots, ix->centroid, ix->chunk_offsets, (int32_t)ix->dim, (int32_t)M, q,
+                lut);
+  orc_query_restore(ix->centroid, (int32_t)ix->dim, q, qr);
+  for (int32_t j = 0; j < topk; ++j) {
+    nns[j] = 0;
+    dists[j] = 0.0f;
+  }
+  *found = 0;
+  B->size = 0;
+  int32_t exps = 0;
+  const int64_t cap = ix->num_pts + 2;
+  int32_t nsel = 0;
+  if (entry >= 0) sel[nsel++] = entry;
+  while (nsel > 0) {
+    for (int32_t b = 0; b < nsel && exps < cap; ++b) {
+      const int64_t u = sel[b];
+      ++exps;
+      const uint8_t* rec = ix->pages + (u / ix->nodes_per_page) * 4096 +
+                           (u % ix->nodes_per_page) * ix->node_len;
+      int32_t deg;
+      memcpy(&deg, rec + data_len, 4);
+      if (deg > R) deg = (int32_t)R;
+      if (deg < 0) deg = 0;
+      const uint8_t* edge = rec + data_len + 4;
+      for (int32_t t = 0; t < deg; ++t) {
+        uint32_t v;
+        memcpy(&v, edge + 4 * t, 4);
+        beam_insert(B, L, orc_adc(lut, (int32_t)M, ix->codes + (int64_t)v * M), v);
+      }
+      topk_push(dists, nns, found, topk, orc_l2(qr, rec, ix->dtype, (int32_t)ix->dim), (int32_t)u);
+    }
+    nsel = 0;
+    if (exps >= cap) break;
+    for (int32_t i = 0; i < B->size && nsel < bw; ++i) {
+      if (B->visited[i]) continue;
+      B->visited[i] = 1;
+      sel[nsel++] = B->id[i];
+    }
+  }
+  if (n_exp) *n_exp = exps;
+}
+
+typedef struct {
+  const orc_index* ix;
+  const float* q;
+  int32_t nq;
+  const int32_t* entries;
+  int32_t topk, L, bw;
+  int32_t *nns, *found, *n_exp;
+  float* dists;
+  int32_t t, nthreads;
+} beam_job;
+
+static void* beam_worker(void* arg) {
+  beam_job* J = (beam_job*)arg;
+  const orc_index* ix = J->ix;
+  float* lut = (float*)malloc(sizeof(float) * (size_t)ix->num_chunks * ORC_NUM_PIVOTS);
+  float* qr = (float*)malloc(sizeof(float) * (size_t)ix->dim);
+  beam_list B;
+  B.dist = (float*)malloc(sizeof(float) * (size_t)J->L);
+  B.id = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)J->L);
+  B.visited = (uint8_t*)malloc((size_t)J->L);
+  int64_t* sel = (int64_t*)malloc(sizeof(int64_t) * (size_t)(J->bw > 1 ? J->bw : 1));
+  for (int32_t qi = J->t; qi < J->nq; qi += J->nthreads) {
+    const float* q = J->q + (int64_t)qi * ix->dim;
+    int32_t entry = J->entries ? J->entries[qi] : orc_entry(ix, q, NULL);
+    int32_t ne = 0;
+    search_beam_one(ix, q, entry, J->topk, J->L, J->bw, J->nns + (int64_t)qi * J->topk,
+                    J->dists + (int64_t)qi * J->topk, J->found + qi, &ne, lut, qr, &B, sel);
+    if (J->n_exp) J->n_exp[qi] = ne;
+  }
+  free(lut);
+  free(qr);
+  free(B.dist);
+  free(B.id);
+  free(B.visited);
+  free(sel);
+  return NULL;
+}
+
+int64_t orc_search_beam(const orc_index* ix, const float* q, int32_t nq, const int32_t* entries,
+                        int32_t topk, int32_t L, int32_t bw, int32_t* nns, float* dists,
+                        int32_t* found, int32_t* n_expansions, int32_t nthreads) {
+  if (nthreads < 1) nthreads = 1;
+  if (bw < 1) bw = 1;
+  pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)nthreads);
+  beam_job* jobs = (beam_job*)calloc((size_t)nthreads, sizeof(beam_job));
+  for (int32_t t = 0; t < nthreads; ++t) {
+    beam_job j = {ix, q, nq, entries, topk, L, bw, nns, found, n_expansions, dists, t, nthreads};
+    jobs[t] = j;
+    pthread_create(&th[t], NULL, beam_worker, &jobs[t]);
+  }
+  for (int32_t t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+  free(jobs);
+  free(th);
+  return 0;
+}
+
 /* ------------------------------------------------------------------ recall */
 
 static int cmp_i32(const void* a, const void* b) {

@@ -89,6 +89,20 @@ int64_t orc_search(const orc_index* ix, const float* q, int32_t nq, const int32_
                    int32_t topk, int32_t L, int32_t* nns, float* dists, int32_t* found,
                    int32_t* n_expansions, int32_t nthreads, int32_t check);
 
+/* Beam search with beam width bw >= 1, a mode of this library with no
+ * counterpart in the reference (which expands one node per iteration).  The
+ * list holds at most L entries sorted by (dist, id), each id once, with a
+ * visited flag.  Each round takes the first bw unvisited entries in list
+ * order (the entry node alone in the first round), marks them visited and
+ * expands them in that order: the PQ (ADC) keys of the node's neighbours
+ * whose ids are not listed are inserted at their lower bounds, the list is
+ * cut back to L, and the node's exact distance is pushed into the top-k
+ * (retset_push_32).  The search ends when no unvisited entry is left.
+ * Arguments as orc_search. */
+int64_t orc_search_beam(const orc_index* ix, const float* q, int32_t nq, const int32_t* entries,
+                        int32_t topk, int32_t L, int32_t bw, int32_t* nns, float* dists,
+                        int32_t* found, int32_t* n_expansions, int32_t nthreads);
+
 /* calc_recall (bin/utils.hpp:104-116): hits of res[i][0..k) in the set of the
  * first k ground-truth ids, over `num` queries, divided by num*k. */
 double orc_recall(const int32_t* res, const int32_t* gt, int32_t num, int32_t gt_dim, int32_t k);

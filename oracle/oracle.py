@@ -47,6 +47,9 @@ def lib():
         L.orc_entry.restype = I32
         L.orc_search.argtypes = [C.POINTER(OrcIndex), P, I32, P, I32, I32, P, P, P, P, I32, I32]
         L.orc_search.restype = I64
+        L.orc_search_beam.argtypes = [C.POINTER(OrcIndex), P, I32, P, I32, I32, I32, P, P, P, P,
+                                      I32]
+        L.orc_search_beam.restype = I64
         L.orc_recall.argtypes = [P, P, I32, I32, I32]
         L.orc_recall.restype = C.c_double
         _lib = L
@@ -188,3 +191,17 @@ class Index:
         v = lib().orc_search(C.byref(self._s), _p(Q), nq, _p(ent), topk, L, _p(nns), _p(d),
                              _p(found), _p(nexp), threads, 1 if check else 0)
         return nns, d, found, nexp, int(v)
+
+    def search_beam(self, Q, topk, L, beam_width, entries=None, threads=1):
+        """Beam search with beam width >= 1 (orc_search_beam); returns
+        (nns, dists, found, n_exp)."""
+        Q = _f32(Q)
+        nq = Q.shape[0]
+        nns = np.empty((nq, topk), np.int32)
+        d = np.empty((nq, topk), np.float32)
+        found = np.empty(nq, np.int32)
+        nexp = np.empty(nq, np.int32)
+        ent = None if entries is None else np.ascontiguousarray(entries, np.int32)
+        lib().orc_search_beam(C.byref(self._s), _p(Q), nq, _p(ent), topk, L, beam_width, _p(nns),
+                              _p(d), _p(found), _p(nexp), threads)
+        return nns, d, found, nexp

@@ -58,3 +58,23 @@ def test_rejects_L_below_topk(tiny_u8):
                         "--data_type", "uint8", "--topk", "10", "--ef_search", "5"],
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=60)
     assert r.returncode != 0 and "ef_search must be >= topk" in r.stdout
+
+
+def test_result_file_and_check_recall(tiny_u8, tmp_path):
+    P = tiny_u8["paths"]
+    res = str(tmp_path / "res.bin")
+    out = _run(["--query", P["query"], "--index", P["index"], "--pq_data", P["pq"], "--data_type",
+                "uint8", "--ground_truth", P["gt"], "--topk", "10", "--ef_search", "40", "-R", "1",
+                "-G", "--result_path", res])
+    reported = float(re.search(r"\[REPORT\] RECALL: ([0-9.]+)", out).group(1))
+    gt = gi.read_vecs(P["gt"], np.int32)
+    ids = np.fromfile(res, dtype=np.int32)
+    nq, k = int(ids[0]), int(ids[1])
+    assert k == 10 and nq * k == ids.size - 2
+    if gt.shape[0] != nq:  # check_recall needs one ground-truth row per result row
+        return
+    r = subprocess.run([os.path.join(ROOT, "gustann_amd", "lib", "check_recall"), res, P["gt"]],
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout
+    m = re.search(r"Recall @ 10: ([0-9.e-]+)", r.stdout)
+    assert m and abs(float(m.group(1)) - reported) < 1e-5
