@@ -205,7 +205,7 @@ def test_argument_errors(u8):
         g.search(Q, 4, 10, 5)  # L < topk
     assert e.value.code == 1
     with pytest.raises(GannError) as e:
-        g.search(Q, 4, 10, 20, beam_width=2)
+        g.search(Q, 4, 10, 20, beam_width=5)  # widths 2..4 are the beam search mode
     assert e.value.code == 6
     nns, d, f = g.search(Q[:0], 0, 10, 20)
     assert nns.shape == (0, 10)
