@@ -20,7 +20,7 @@ ABI_SYMBOLS = (
     "gann_last_error", "gann_version", "gann_open", "gann_close", "gann_get_info",
     "gann_search", "gann_search_ex", "gann_search_device", "gann_search_device_ex", "gann_nav_entry",
     "gann_pq_open", "gann_pq_create", "gann_pq_close", "gann_handle_pq",
-    "gann_pq_lut_build", "gann_pq_adc_scan", "gann_pq_adc_scan_device",
+    "gann_pq_lut_build", "gann_pq_adc_scan", "gann_pq_adc_scan_device", "gann_knn_exact",
 )
 
 
@@ -62,6 +62,7 @@ _SIGS = {
     "gann_search_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P,
                                  C.POINTER(Stats)]),
     "gann_search_device": (C.c_int, [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P]),
+    "gann_knn_exact": (C.c_int, [_P, _I64, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "gann_search_device_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P,
                                         _P, _P]),
     "gann_nav_entry": (C.c_int, [_P, _P, _I32, _P, _P]),

@@ -49,7 +49,7 @@ def build_hip(verbose=False):
     objdir = os.path.join(ROOT, "_build")
     os.makedirs(objdir, exist_ok=True)
     objs = []
-    for src in ("gann_kernels.hip", "gann_api.cpp"):
+    for src in ("gann_kernels.hip", "gann_knn.hip", "gann_api.cpp"):
         obj = os.path.join(objdir, src.rsplit(".", 1)[0] + ".o")
         _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
         objs.append(obj)

@@ -20,6 +20,7 @@
 
 #include "formats.hpp"
 #include "gann_kernels.hpp"
+#include "gann_knn.hpp"
 
 namespace {
 
@@ -793,6 +794,108 @@ int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const i
     check_lds(gann::adc_smem_bytes(pq->dev.M, pq->dev.dim), pq->device, "ADC scan");
     hipStream_t s = (hipStream_t)stream;
     GANN_HIP(gann::launch_pq_adc_scan(pq->dev, q_dev, nq, ids_dev, ids_per_q, out_dev, s));
+  });
+}
+
+
+int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, const float* queries,
+                   int32_t nq, int32_t k, int32_t device_id, int32_t* ids, float* dists) {
+  return guarded([&] {
+    if (dtype != GANN_UINT8 && dtype != GANN_FLOAT) raise(GANN_ERR_INVALID, "unknown data type");
+    if (n < 1 || nq < 0) raise(GANN_ERR_INVALID, "need n >= 1 and nq >= 0");
+    if (dim < 1 || dim > 256) raise(GANN_ERR_UNSUPPORTED, "dim must be in [1, 256]");
+    if (k < 1 || k > 128) raise(GANN_ERR_UNSUPPORTED, "k must be in [1, 128]");
+    if (n > (int64_t)INT32_MAX) raise(GANN_ERR_UNSUPPORTED, "ids are int32: n must be < 2^31");
+    if (nq == 0) return;
+    if (!base || !queries || !ids || !dists) raise(GANN_ERR_INVALID, "NULL buffer");
+    const bool u8 = dtype == GANN_UINT8;
+    if (u8)
+      for (int64_t i = 0; i < (int64_t)nq * dim; ++i) {
+        const float v = queries[i];
+        if (!(v >= 0.0f && v <= 255.0f) || v != std::floor(v))
+          raise(GANN_ERR_INVALID, "uint8 queries must hold integers in [0, 255]");
+      }
+    GANN_HIP(hipSetDevice(device_id));
+    int cus = 0;
+    GANN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_id));
+    const int QB = gann::knn_queries_per_block();
+    const int nqp = (nq + QB - 1) / QB * QB;
+    const int dp = (dim + 31) / 32 * 32;
+    const size_t elem = u8 ? 1 : 4;
+    const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t)1 << 31) / (dim * (int64_t)elem)));
+    const int64_t qblocks = nqp / QB;
+    // about 8 wavefronts per CU, each slice at least 1024 points
+    int64_t slices = std::max<int64_t>(1, std::min<int64_t>((8LL * cus + qblocks - 1) / qblocks,
+                                                           (chunk + 1023) / 1024));
+    const int64_t slice_len = ((chunk + slices - 1) / slices + 31) / 32 * 32;
+    slices = (chunk + slice_len - 1) / slice_len;
+    DevBuf raw, xs, xn, qs, qn, qf, pd, pi;
+    raw.ensure((size_t)chunk * dim * elem);
+    pd.ensure((size_t)slices * nq * k * 4);
+    pi.ensure((size_t)slices * nq * k * 4);
+    if (u8) {
+      std::vector<int8_t> hq((size_t)nqp * dp, 0);
+      std::vector<int32_t> hn((size_t)nqp, 0);
+      for (int32_t q = 0; q < nq; ++q) {
+        int32_t sum = 0;
+        for (int32_t d = 0; d < dim; ++d) {
+          const int v = (int)queries[(size_t)q * dim + d] - 128;
+          hq[(size_t)q * dp + d] = (int8_t)v;
+          sum += v * v;
+        }
+        hn[(size_t)q] = sum;
+      }
+      xs.ensure((size_t)chunk * dp);
+      xn.ensure((size_t)chunk * 4);
+      qs.ensure(hq.size());
+      qn.ensure(hn.size() * 4);
+      GANN_HIP(hipMemcpy(qs.p, hq.data(), hq.size(), hipMemcpyHostToDevice));
+      GANN_HIP(hipMemcpy(qn.p, hn.data(), hn.size() * 4, hipMemcpyHostToDevice));
+    } else {
+      qf.ensure((size_t)nq * dim * 4);
+      GANN_HIP(hipMemcpy(qf.p, queries, (size_t)nq * dim * 4, hipMemcpyHostToDevice));
+    }
+    check_lds(gann::knn_smem_bytes(u8 ? 0 : 1, dim, k), device_id, "exact k-NN");
+    std::vector<float> bd((size_t)nq * k, INFINITY), hd((size_t)slices * nq * k);
+    std::vector<int32_t> bi((size_t)nq * k, -1), hi((size_t)slices * nq * k);
+    std::vector<std::pair<float, int32_t>> cand;
+    for (int64_t off = 0; off < n; off += chunk) {
+      const int64_t cn = std::min(chunk, n - off);
+      const int64_t cs = (cn + slice_len - 1) / slice_len;
+      GANN_HIP(hipMemcpy(raw.p, (const uint8_t*)base + (size_t)off * dim * elem, (size_t)cn * dim * elem,
+                         hipMemcpyHostToDevice));
+      if (u8) {
+        GANN_HIP(gann::launch_knn_prep_u8(raw.as<uint8_t>(), cn, dim, dp, xs.as<int8_t>(),
+                                          xn.as<int32_t>(), 0));
+        GANN_HIP(gann::launch_knn_u8(xs.as<int8_t>(), xn.as<int32_t>(), cn, dp, qs.as<int8_t>(),
+                                     qn.as<int32_t>(), nq, k, cs, slice_len, off, pd.as<float>(),
+                                     pi.as<int32_t>(), 0));
+      } else {
+        GANN_HIP(gann::launch_knn_f32(raw.as<float>(), cn, dim, qf.as<float>(), nq, k, cs, slice_len,
+                                      off, pd.as<float>(), pi.as<int32_t>(), 0));
+      }
+      GANN_HIP(hipMemcpy(hd.data(), pd.p, (size_t)cs * nq * k * 4, hipMemcpyDeviceToHost));
+      GANN_HIP(hipMemcpy(hi.data(), pi.p, (size_t)cs * nq * k * 4, hipMemcpyDeviceToHost));
+      for (int32_t q = 0; q < nq; ++q) {
+        cand.clear();
+        for (int32_t j = 0; j < k; ++j)
+          if (bi[(size_t)q * k + j] >= 0) cand.emplace_back(bd[(size_t)q * k + j], bi[(size_t)q * k + j]);
+        for (int64_t sl = 0; sl < cs; ++sl)
+          for (int32_t j = 0; j < k; ++j) {
+            const size_t o = ((size_t)sl * nq + q) * k + j;
+            if (hi[o] >= 0) cand.emplace_back(hd[o], hi[o]);
+          }
+        const size_t keep = std::min<size_t>(cand.size(), (size_t)k);
+        std::partial_sort(cand.begin(), cand.begin() + keep, cand.end());
+        for (int32_t j = 0; j < k; ++j) {
+          const bool ok = (size_t)j < keep;
+          bd[(size_t)q * k + j] = ok ? cand[(size_t)j].first : INFINITY;
+          bi[(size_t)q * k + j] = ok ? cand[(size_t)j].second : -1;
+        }
+      }
+    }
+    std::memcpy(ids, bi.data(), bi.size() * 4);
+    std::memcpy(dists, bd.data(), bd.size() * 4);
   });
 }
 

@@ -1,0 +1,323 @@
+// Exact k-nearest-neighbour search by squared L2 (ties broken by the smaller
+// id): the ground truth that recall is measured against.  The reference
+// takes its ground truth from external tools; this is the GPU counterpart of
+// the repository's CPU brute force (index_builder.cpp gib_brute_force).
+//
+// One wavefront owns 32 queries and a slice of the base set and scans it in
+// tiles of 32 points.
+//  * uint8: the 32x32 tile of dot products comes from v_mfma_i32_32x32x32_i8
+//    on x - 128 and q - 128 (int8), so ||q - x||^2 = |q'|^2 + |x'|^2 - 2 q'.x'
+//    is exact in int32 (at most 256 * 255^2 < 2^24, exact again as float).
+//  * float: every lane forms 16 distances directly, sum over the dims in
+//    ascending order of fma(t, t, s), t = q - x.
+// A distance below the query's current k-th best is appended to the query's
+// LDS buffer; a buffer that could overflow with the next tile is cut back to
+// its k best by rank.  Points are scanned in increasing id order, so a tie
+// with the k-th best loses to it.  Each wavefront writes its sorted k best
+// per query; the host merges the slices.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "gann_device.hpp"
+#include "gann_knn.hpp"
+
+namespace gann {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kQB = 32;  // queries per wavefront (MFMA rows)
+constexpr int kTP = 32;  // points per tile (MFMA columns)
+
+__device__ __forceinline__ bool cand_lt(float da, int32_t ia, float db, int32_t ib) {
+  return da < db || (da == db && ia < ib);
+}
+
+// Row of accumulator register i of this lane in a 32x32 MFMA result (the
+// column is lane % 32).
+__device__ __forceinline__ int acc_row(int i, int lane) {
+  return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+}
+
+// Per-wavefront candidate buffers: query m keeps entries [0, cnt[m]) of
+// bd/bi[m * cap ...]; thr[m] is the k-th smallest kept distance once k are
+// kept (+inf before).  cap = k + 64 >= k + one tile.
+struct KnnBuf {
+  float* bd;
+  int32_t* bi;
+  int32_t* cnt;
+  float* thr;
+  int cap, k;
+
+  __device__ void init() {
+    const int lane = lane_id();
+    if (lane < kQB) {
+      cnt[lane] = 0;
+      thr[lane] = INFINITY;
+    }
+    wave_sync();
+  }
+
+  // Keeps the k smallest (dist, id) of query m, sorted.
+  __device__ void compact(int m) {
+    const int lane = lane_id();
+    const int n = cnt[m];
+    float* d_m = bd + (size_t)m * cap;
+    int32_t* i_m = bi + (size_t)m * cap;
+    float d[3];
+    int32_t id[3];
+    int rk[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int e = lane + kWave * j;
+      d[j] = e < n ? d_m[e] : INFINITY;
+      id[j] = e < n ? i_m[e] : -1;
+      rk[j] = 0;
+    }
+    for (int e2 = 0; e2 < n; ++e2) {
+      const float d2 = d_m[e2];
+      const int32_t i2 = i_m[e2];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) rk[j] += cand_lt(d2, i2, d[j], id[j]) ? 1 : 0;
+    }
+    wave_sync();
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int e = lane + kWave * j;
+      if (e < n && rk[j] < k) {
+        d_m[rk[j]] = d[j];
+        i_m[rk[j]] = id[j];
+      }
+    }
+    wave_sync();
+    if (lane == 0) {
+      cnt[m] = min(n, k);
+      thr[m] = n >= k ? d_m[k - 1] : INFINITY;
+    }
+    wave_sync();
+  }
+
+  // Cuts back every buffer that could overflow with one more tile; returns
+  // whether any was cut.
+  __device__ bool maybe_compact() {
+    const int lane = lane_id();
+    uint64_t need = ballot64(lane < kQB && cnt[lane] > cap - kTP);
+    const bool any = need != 0;
+    while (need) {
+      const int m = (int)__builtin_ctzll(need);
+      need &= need - 1;
+      compact(m);
+    }
+    return any;
+  }
+
+  __device__ void finish(int q0, int nq, int64_t slice, float* part_d, int32_t* part_i) {
+    const int lane = lane_id();
+    for (int m = 0; m < kQB && q0 + m < nq; ++m) {
+      compact(m);
+      const int n = cnt[m];
+      const int64_t o = (slice * nq + q0 + m) * (int64_t)k;
+      for (int j = lane; j < k; j += kWave) {
+        part_d[o + j] = j < n ? bd[(size_t)m * cap + j] : INFINITY;
+        part_i[o + j] = j < n ? bi[(size_t)m * cap + j] : -1;
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ KnnBuf knn_buf(uint8_t* smem, int k) {
+  KnnBuf B;
+  B.k = k;
+  B.cap = k + 64;
+  B.bd = reinterpret_cast<float*>(smem);
+  B.bi = reinterpret_cast<int32_t*>(B.bd + (size_t)kQB * B.cap);
+  B.cnt = B.bi + (size_t)kQB * B.cap;
+  B.thr = reinterpret_cast<float*>(B.cnt + kQB);
+  return B;
+}
+
+// x - 128 as int8, rows padded with zeros to dp bytes, and |x - 128|^2.
+__global__ void knn_prep_u8_kernel(const uint8_t* __restrict__ x, int64_t n, int dim, int dp,
+                                   int8_t* __restrict__ xs, int32_t* __restrict__ xn) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int32_t s = 0;
+  for (int d = 0; d < dp; ++d) {
+    const int v = d < dim ? (int)x[i * dim + d] - 128 : 0;
+    xs[i * dp + d] = (int8_t)v;
+    s += v * v;
+  }
+  xn[i] = s;
+}
+
+template <int STEPS>
+__global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ xs,
+                                                    const int32_t* __restrict__ xn, int64_t n,
+                                                    const int8_t* __restrict__ qs,
+                                                    const int32_t* __restrict__ qn, int nq, int k,
+                                                    int64_t slice_len, int64_t id_base,
+                                                    float* __restrict__ part_d,
+                                                    int32_t* __restrict__ part_i) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  constexpr int dp = 32 * STEPS;
+  const int lane = lane_id();
+  const int q0 = blockIdx.x * kQB;
+  const int64_t slice = blockIdx.y;
+  const int64_t start = slice * slice_len, end = min(n, start + slice_len);
+  KnnBuf B = knn_buf(smem_raw, k);
+  B.init();
+  // A: query q0 + lane % 32, bytes 16 * (lane / 32) + 32 s (query rows are
+  // padded to a multiple of 32 on the host)
+  v4i a[STEPS];
+  const int8_t* qrow = qs + (size_t)(q0 + (lane & 31)) * dp + 16 * (lane >> 5);
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) a[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
+  int32_t qn_r[16];
+  float thr_r[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    qn_r[i] = qn[q0 + acc_row(i, lane)];
+    thr_r[i] = INFINITY;
+  }
+  for (int64_t t0 = start; t0 < end; t0 += kTP) {
+    const int64_t p = t0 + (lane & 31);
+    const bool valid = p < end;
+    v4i b[STEPS];
+    const int8_t* xrow = xs + (valid ? p : start) * dp + 16 * (lane >> 5);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) b[s] = *reinterpret_cast<const v4i*>(xrow + 32 * s);
+    v16i acc = {};
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], b[s], acc, 0, 0, 0);
+    const int32_t xnv = xn[valid ? p : start];
+    const int32_t xnp = valid ? xnv : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int m = acc_row(i, lane);
+      const float dist = (float)(qn_r[i] + xnp - 2 * acc[i]);
+      if (valid && q0 + m < nq && dist < thr_r[i]) {
+        const int slot = atomicAdd(&B.cnt[m], 1);
+        B.bd[(size_t)m * B.cap + slot] = dist;
+        B.bi[(size_t)m * B.cap + slot] = (int32_t)(p + id_base);
+      }
+    }
+    wave_sync();
+    if (B.maybe_compact()) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) thr_r[i] = B.thr[acc_row(i, lane)];
+    }
+  }
+  B.finish(q0, nq, slice, part_d, part_i);
+}
+
+// Float: the 32 queries of the wavefront in LDS after the buffers.
+__global__ __launch_bounds__(64) void knn_f32_kernel(const float* __restrict__ x, int64_t n,
+                                                     int dim, const float* __restrict__ q, int nq,
+                                                     int k, int64_t slice_len, int64_t id_base,
+                                                     float* __restrict__ part_d,
+                                                     int32_t* __restrict__ part_i) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  const int lane = lane_id();
+  const int q0 = blockIdx.x * kQB;
+  const int64_t slice = blockIdx.y;
+  const int64_t start = slice * slice_len, end = min(n, start + slice_len);
+  KnnBuf B = knn_buf(smem_raw, k);
+  float* qt = reinterpret_cast<float*>(B.thr + kQB);
+  for (int e = lane; e < kQB * dim; e += kWave) {
+    const int m = e / dim;
+    qt[e] = q0 + m < nq ? q[(size_t)(q0 + m) * dim + (e - m * dim)] : 0.0f;
+  }
+  B.init();
+  float thr_r[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) thr_r[i] = INFINITY;
+  for (int64_t t0 = start; t0 < end; t0 += kTP) {
+    const int64_t p = t0 + (lane & 31);
+    const bool valid = p < end;
+    const float* xr = x + (size_t)(valid ? p : start) * dim;
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    for (int d = 0; d < dim; ++d) {
+      const float xv = xr[d];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float t = qt[acc_row(i, lane) * dim + d] - xv;
+        acc[i] = fma_f(t, t, acc[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int m = acc_row(i, lane);
+      if (valid && q0 + m < nq && acc[i] < thr_r[i]) {
+        const int slot = atomicAdd(&B.cnt[m], 1);
+        B.bd[(size_t)m * B.cap + slot] = acc[i];
+        B.bi[(size_t)m * B.cap + slot] = (int32_t)(p + id_base);
+      }
+    }
+    wave_sync();
+    if (B.maybe_compact()) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) thr_r[i] = B.thr[acc_row(i, lane)];
+    }
+  }
+  B.finish(q0, nq, slice, part_d, part_i);
+}
+
+size_t knn_buf_bytes(int k) { return (size_t)kQB * (k + 64) * 8 + (size_t)kQB * 8; }
+
+}  // namespace
+
+int knn_queries_per_block() { return kQB; }
+
+size_t knn_smem_bytes(int dtype, int dim, int k) {
+  return knn_buf_bytes(k) + (dtype == 0 ? 0 : (size_t)kQB * dim * 4);
+}
+
+hipError_t launch_knn_prep_u8(const uint8_t* x, int64_t n, int dim, int dp, int8_t* xs, int32_t* xn,
+                              hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(knn_prep_u8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x,
+                     n, dim, dp, xs, xn);
+  return hipGetLastError();
+}
+
+hipError_t launch_knn_u8(const int8_t* xs, const int32_t* xn, int64_t n, int dp, const int8_t* qs,
+                         const int32_t* qn, int nq, int k, int64_t slices, int64_t slice_len,
+                         int64_t id_base, float* part_d, int32_t* part_i, hipStream_t stream) {
+  const dim3 grid((unsigned)((nq + kQB - 1) / kQB), (unsigned)slices);
+  const size_t smem = knn_smem_bytes(0, dp, k);
+  switch (dp / 32) {
+#define GANN_KNN_CASE(S)                                                                      \
+  case S:                                                                                     \
+    hipLaunchKernelGGL(knn_u8_kernel<S>, grid, dim3(64), smem, stream, xs, xn, n, qs, qn, nq, \
+                       k, slice_len, id_base, part_d, part_i);                                \
+    break;
+    GANN_KNN_CASE(1)
+    GANN_KNN_CASE(2)
+    GANN_KNN_CASE(3)
+    GANN_KNN_CASE(4)
+    GANN_KNN_CASE(5)
+    GANN_KNN_CASE(6)
+    GANN_KNN_CASE(7)
+    GANN_KNN_CASE(8)
+#undef GANN_KNN_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_knn_f32(const float* x, int64_t n, int dim, const float* q, int nq, int k,
+                          int64_t slices, int64_t slice_len, int64_t id_base, float* part_d,
+                          int32_t* part_i, hipStream_t stream) {
+  const dim3 grid((unsigned)((nq + kQB - 1) / kQB), (unsigned)slices);
+  hipLaunchKernelGGL(knn_f32_kernel, grid, dim3(64), knn_smem_bytes(1, dim, k), stream, x, n, dim,
+                     q, nq, k, slice_len, id_base, part_d, part_i);
+  return hipGetLastError();
+}
+
+}  // namespace gann

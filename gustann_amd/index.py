@@ -120,6 +120,23 @@ def brute_force_knn(X: np.ndarray, Q: np.ndarray, k: int, threads=None):
     return ids, d
 
 
+def brute_force_knn_gpu(X: np.ndarray, Q: np.ndarray, k: int, device_id: int = 0):
+    """The same exact k-NN on the GPU (gann_knn_exact: int8 MFMA for uint8 data,
+    exact; fma chains for float).  Returns (ids, dists)."""
+    from . import _native as N
+    X = np.ascontiguousarray(X)
+    Q = np.ascontiguousarray(Q, np.float32)
+    n, dim = X.shape
+    dtype = N.UINT8 if X.dtype == np.uint8 else N.FLOAT
+    if dtype == N.FLOAT:
+        X = np.ascontiguousarray(X, np.float32)
+    ids = np.empty((Q.shape[0], k), np.int32)
+    d = np.empty((Q.shape[0], k), np.float32)
+    N.check(N.hip_lib().gann_knn_exact(_ptr(X), n, dim, dtype, _ptr(Q), Q.shape[0], k, device_id,
+                                       _ptr(ids), _ptr(d)))
+    return ids, d
+
+
 # ------------------------------------------------------------------ writers
 
 def write_disk_index(path, X, nbr, deg, medoid):

@@ -158,6 +158,20 @@ int gann_pq_adc_scan(gann_pq* pq, const float* q, int32_t nq, const int32_t* ids
 int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const int32_t* ids_dev,
                             int32_t ids_per_q, float* out_dev, void* stream);
 
+/* ---- exact nearest neighbours (ground truth) */
+
+/* Exact k nearest neighbours of each query by squared L2, ties broken by the
+ * smaller id: the ground truth that calc_recall (bin/utils.hpp:104-116)
+ * scores against, stored by callers as ivecs.  No counterpart in the
+ * reference, whose ground truth comes from external tools; it serves
+ * dataset builders and tests.  base: [n][dim] on the host, uint8
+ * (GANN_UINT8; queries must then hold integers in [0, 255]; distances exact)
+ * or f32 (GANN_FLOAT; each distance sums fma((q - x)^2) over the dims in
+ * ascending order); queries [nq][dim] f32 on the host; ids/dists [nq][k] on
+ * the host, id -1 and +inf past n.  dim <= 256, k <= 128, n < 2^31. */
+int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, const float* queries,
+                   int32_t nq, int32_t k, int32_t device_id, int32_t* ids, float* dists);
+
 #ifdef __cplusplus
 }
 #endif
