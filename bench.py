@@ -256,6 +256,49 @@ def bench_search(args):
     return result
 
 
+MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8
+
+
+def bench_knn(args):
+    """Exact k-NN (ground truth) of nq uint8 queries over n uint8 points
+    (gann_knn_exact, int8 MFMA).  Timed end to end (base upload, kernels,
+    host merge of the slices); operations counted as 2 * n * nq * dim int8
+    multiply-adds."""
+    import torch  # noqa: F401  (device runtime first)
+    from gustann_amd import index as gi
+    n, dim, nq, k = args.n, args.dim, args.nq, args.knn_k
+    r = np.random.default_rng(7)
+    X = r.integers(0, 256, (n, dim), dtype=np.uint8)
+    Q = r.integers(0, 256, (nq, dim), dtype=np.uint8).astype(np.float32)
+    for _ in range(args.warmup):
+        gi.brute_force_knn_gpu(X, Q, k)
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        ids, d = gi.brute_force_knn_gpu(X, Q, k)
+    dt = (time.perf_counter() - t) / args.steps
+    ops = 2.0 * n * nq * dim
+    result = {
+        "metric": "exact k-NN queries/s (ground truth)", "value": nq / dt, "unit": "queries/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": dt * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8",
+        "data": "synthetic uniform uint8",
+        "config": {"workload": f"exact_knn_{n}x{dim}_u8_nq{nq}_k{k}"},
+        "roofline": {"bound": "mfma", "achieved": ops / dt / 1e12, "peak": MFMA_I8_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": ops / dt / 1e12 / MFMA_I8_PEAK_TOPS, "traffic": None},
+    }
+    if not args.no_cpu:
+        m = max(1, min(nq, 64))
+        t = time.perf_counter()
+        c_ids, c_d = gi.brute_force_knn(X, Q[:m], k, threads=min(16, os.cpu_count() or 1))
+        cdt = time.perf_counter() - t
+        result["cpu_baseline"] = {"value": m / cdt, "unit": "queries/s",
+                                  "cores": min(16, os.cpu_count() or 1), "kind": "port",
+                                  "sample": f"first {m} queries: gib_brute_force, {cdt:.1f} s"}
+        result["parity_sample_bitexact"] = bool(np.array_equal(c_ids, ids[:m]) and
+                                                np.array_equal(c_d, d[:m]))
+    return result
+
+
 def bench_copy(args):
     """Calibration kernel for the HBM traffic counters: one device-to-device
     copy of a buffer of known size (reads and writes copy_bytes each)."""
@@ -283,7 +326,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["adc", "search", "copy"], default="adc")
+    ap.add_argument("--workload", choices=["adc", "search", "copy", "knn"], default="adc")
+    ap.add_argument("--knn-k", type=int, default=100)
     ap.add_argument("--copy-bytes", type=int, default=1 << 31)
     ap.add_argument("--nq", type=int, default=10000)
     ap.add_argument("--ids-per-query", type=int, default=4096)
@@ -316,7 +360,7 @@ def main():
     if args.workload == "copy":
         res = bench_copy(args)
     else:
-        res = bench_adc(args) if args.workload == "adc" else bench_search(args)
+        res = {"adc": bench_adc, "search": bench_search, "knn": bench_knn}[args.workload](args)
     print(json.dumps(res), flush=True)
 
 

@@ -32,22 +32,23 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kQB = 32;  // queries per wavefront (MFMA rows)
 constexpr int kTP = 32;  // points per tile (MFMA columns)
 
-__device__ __forceinline__ bool cand_lt(float da, int32_t ia, float db, int32_t ib) {
-  return da < db || (da == db && ia < ib);
-}
-
 // Row of accumulator register i of this lane in a 32x32 MFMA result (the
 // column is lane % 32).
 __device__ __forceinline__ int acc_row(int i, int lane) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
 }
 
-// Per-wavefront candidate buffers: query m keeps entries [0, cnt[m]) of
-// bd/bi[m * cap ...]; thr[m] is the k-th smallest kept distance once k are
-// kept (+inf before).  cap = k + 64 >= k + one tile.
+// Candidate key: bits(dist) << 32 | id.  Distances are non-negative and ids
+// non-negative, so one unsigned compare orders (dist, id) lexicographically.
+__device__ __forceinline__ uint64_t cand_key(float d, int32_t id) {
+  return ((uint64_t)__float_as_uint(d) << 32) | (uint32_t)id;
+}
+
+// Per-wavefront candidate buffers: query m keeps keys [0, cnt[m]) of
+// bk[m * cap ...]; thr[m] is the k-th smallest kept distance once k are kept
+// (+inf before).  cap = k + 64 >= k + one tile.
 struct KnnBuf {
-  float* bd;
-  int32_t* bi;
+  uint64_t* bk;
   int32_t* cnt;
   float* thr;
   int cap, k;
@@ -61,41 +62,41 @@ struct KnnBuf {
     wave_sync();
   }
 
-  // Keeps the k smallest (dist, id) of query m, sorted.
+  __device__ __forceinline__ void append(int m, float d, int32_t id) {
+    const int slot = atomicAdd(&cnt[m], 1);
+    bk[(size_t)m * cap + slot] = cand_key(d, id);
+  }
+
+  // Keeps the k smallest keys of query m, sorted (each key's rank is the
+  // number of smaller keys).
   __device__ void compact(int m) {
     const int lane = lane_id();
     const int n = cnt[m];
-    float* d_m = bd + (size_t)m * cap;
-    int32_t* i_m = bi + (size_t)m * cap;
-    float d[3];
-    int32_t id[3];
+    uint64_t* k_m = bk + (size_t)m * cap;
+    uint64_t v[3];
     int rk[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       const int e = lane + kWave * j;
-      d[j] = e < n ? d_m[e] : INFINITY;
-      id[j] = e < n ? i_m[e] : -1;
+      v[j] = e < n ? k_m[e] : ~(uint64_t)0;
       rk[j] = 0;
     }
+#pragma unroll 8
     for (int e2 = 0; e2 < n; ++e2) {
-      const float d2 = d_m[e2];
-      const int32_t i2 = i_m[e2];
+      const uint64_t w = k_m[e2];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) rk[j] += cand_lt(d2, i2, d[j], id[j]) ? 1 : 0;
+      for (int j = 0; j < 3; ++j) rk[j] += w < v[j] ? 1 : 0;
     }
     wave_sync();
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       const int e = lane + kWave * j;
-      if (e < n && rk[j] < k) {
-        d_m[rk[j]] = d[j];
-        i_m[rk[j]] = id[j];
-      }
+      if (e < n && rk[j] < k) k_m[rk[j]] = v[j];
     }
     wave_sync();
     if (lane == 0) {
       cnt[m] = min(n, k);
-      thr[m] = n >= k ? d_m[k - 1] : INFINITY;
+      thr[m] = n >= k ? __uint_as_float((uint32_t)(k_m[k - 1] >> 32)) : INFINITY;
     }
     wave_sync();
   }
@@ -121,8 +122,9 @@ struct KnnBuf {
       const int n = cnt[m];
       const int64_t o = (slice * nq + q0 + m) * (int64_t)k;
       for (int j = lane; j < k; j += kWave) {
-        part_d[o + j] = j < n ? bd[(size_t)m * cap + j] : INFINITY;
-        part_i[o + j] = j < n ? bi[(size_t)m * cap + j] : -1;
+        const uint64_t key = j < n ? bk[(size_t)m * cap + j] : 0;
+        part_d[o + j] = j < n ? __uint_as_float((uint32_t)(key >> 32)) : INFINITY;
+        part_i[o + j] = j < n ? (int32_t)(uint32_t)key : -1;
       }
     }
   }
@@ -132,9 +134,8 @@ __device__ __forceinline__ KnnBuf knn_buf(uint8_t* smem, int k) {
   KnnBuf B;
   B.k = k;
   B.cap = k + 64;
-  B.bd = reinterpret_cast<float*>(smem);
-  B.bi = reinterpret_cast<int32_t*>(B.bd + (size_t)kQB * B.cap);
-  B.cnt = B.bi + (size_t)kQB * B.cap;
+  B.bk = reinterpret_cast<uint64_t*>(smem);
+  B.cnt = reinterpret_cast<int32_t*>(B.bk + (size_t)kQB * B.cap);
   B.thr = reinterpret_cast<float*>(B.cnt + kQB);
   return B;
 }
@@ -152,6 +153,48 @@ __global__ void knn_prep_u8_kernel(const uint8_t* __restrict__ x, int64_t n, int
   }
   xn[i] = s;
 }
+
+// The same for dim == dp (a multiple of 32): one thread per 16 bytes, the
+// norm accumulated with an atomic add per chunk (xn zeroed first).
+__global__ void knn_prep_u8_wide_kernel(const uint4* __restrict__ x, int64_t chunks, int cpr,
+                                        uint4* __restrict__ xs, int32_t* __restrict__ xn) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= chunks) return;
+  const uint4 v = x[c];
+  const uint32_t w[4] = {v.x ^ 0x80808080u, v.y ^ 0x80808080u, v.z ^ 0x80808080u,
+                         v.w ^ 0x80808080u};
+  int32_t s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int t = (int)(int8_t)(uint8_t)(w[j] >> (8 * b));
+      s += t * t;
+    }
+  xs[c] = make_uint4(w[0], w[1], w[2], w[3]);
+  atomicAdd(&xn[c / cpr], s);
+}
+
+// One 32-point tile of B operands (lane: point t0 + lane % 32, bytes
+// 16 * (lane / 32) + 32 s) and the point's |x'|^2; points past `end` read
+// row `start` and are marked invalid.
+template <int STEPS>
+struct KnnTile {
+  v4i b[STEPS];
+  int32_t xn;
+  bool valid;
+  __device__ __forceinline__ void load(const int8_t* xs, const int32_t* xnorm, int64_t t0,
+                                       int64_t start, int64_t end, int lane) {
+    constexpr int dp = 32 * STEPS;
+    const int64_t p = t0 + (lane & 31);
+    const int64_t r = p < end ? p : start;
+    const int8_t* xrow = xs + r * dp + 16 * (lane >> 5);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) b[s] = *reinterpret_cast<const v4i*>(xrow + 32 * s);
+    xn = xnorm[r];
+    valid = p < end;
+  }
+};
 
 template <int STEPS>
 __global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ xs,
@@ -175,40 +218,47 @@ __global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ x
   const int8_t* qrow = qs + (size_t)(q0 + (lane & 31)) * dp + 16 * (lane >> 5);
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) a[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
-  int32_t qn_r[16];
-  float thr_r[16];
+  // distances are exact integers: thresholds in int32 (rows past nq take
+  // nothing)
+  int32_t qn_r[16], thr_r[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    qn_r[i] = qn[q0 + acc_row(i, lane)];
-    thr_r[i] = INFINITY;
+    const int m = acc_row(i, lane);
+    qn_r[i] = qn[q0 + m];
+    thr_r[i] = q0 + m < nq ? INT32_MAX : INT32_MIN;
   }
+  KnnTile<STEPS> cur, nxt;
+  if (start < end) cur.load(xs, xn, start, start, end, lane);
   for (int64_t t0 = start; t0 < end; t0 += kTP) {
-    const int64_t p = t0 + (lane & 31);
-    const bool valid = p < end;
-    v4i b[STEPS];
-    const int8_t* xrow = xs + (valid ? p : start) * dp + 16 * (lane >> 5);
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) b[s] = *reinterpret_cast<const v4i*>(xrow + 32 * s);
+    if (t0 + kTP < end) nxt.load(xs, xn, t0 + kTP, start, end, lane);  // next tile in flight
     v16i acc = {};
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], b[s], acc, 0, 0, 0);
-    const int32_t xnv = xn[valid ? p : start];
-    const int32_t xnp = valid ? xnv : 0;
+    for (int s = 0; s < STEPS; ++s)
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], cur.b[s], acc, 0, 0, 0);
+    int32_t dist[16];
+    uint64_t any = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int m = acc_row(i, lane);
-      const float dist = (float)(qn_r[i] + xnp - 2 * acc[i]);
-      if (valid && q0 + m < nq && dist < thr_r[i]) {
-        const int slot = atomicAdd(&B.cnt[m], 1);
-        B.bd[(size_t)m * B.cap + slot] = dist;
-        B.bi[(size_t)m * B.cap + slot] = (int32_t)(p + id_base);
+      dist[i] = qn_r[i] + cur.xn - 2 * acc[i];
+      any |= ballot64(cur.valid && dist[i] < thr_r[i]);
+    }
+    if (any) {
+      const int32_t id = (int32_t)(t0 + (lane & 31) + id_base);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (cur.valid && dist[i] < thr_r[i]) B.append(acc_row(i, lane), (float)dist[i], id);
+      }
+      wave_sync();
+      if (B.maybe_compact()) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int m = acc_row(i, lane);
+          const float t = B.thr[m];
+          if (q0 + m < nq) thr_r[i] = t == INFINITY ? INT32_MAX : (int32_t)t;
+        }
       }
     }
-    wave_sync();
-    if (B.maybe_compact()) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) thr_r[i] = B.thr[acc_row(i, lane)];
-    }
+    cur = nxt;
   }
   B.finish(q0, nq, slice, part_d, part_i);
 }
@@ -252,11 +302,7 @@ __global__ __launch_bounds__(64) void knn_f32_kernel(const float* __restrict__ x
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int m = acc_row(i, lane);
-      if (valid && q0 + m < nq && acc[i] < thr_r[i]) {
-        const int slot = atomicAdd(&B.cnt[m], 1);
-        B.bd[(size_t)m * B.cap + slot] = acc[i];
-        B.bi[(size_t)m * B.cap + slot] = (int32_t)(p + id_base);
-      }
+      if (valid && q0 + m < nq && acc[i] < thr_r[i]) B.append(m, acc[i], (int32_t)(p + id_base));
     }
     wave_sync();
     if (B.maybe_compact()) {
@@ -280,6 +326,16 @@ size_t knn_smem_bytes(int dtype, int dim, int k) {
 hipError_t launch_knn_prep_u8(const uint8_t* x, int64_t n, int dim, int dp, int8_t* xs, int32_t* xn,
                               hipStream_t stream) {
   if (n <= 0) return hipSuccess;
+  if (dim == dp) {
+    hipError_t e = hipMemsetAsync(xn, 0, (size_t)n * 4, stream);
+    if (e != hipSuccess) return e;
+    const int cpr = dp / 16;
+    const int64_t chunks = n * cpr;
+    hipLaunchKernelGGL(knn_prep_u8_wide_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                       stream, reinterpret_cast<const uint4*>(x), chunks, cpr,
+                       reinterpret_cast<uint4*>(xs), xn);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(knn_prep_u8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x,
                      n, dim, dp, xs, xn);
   return hipGetLastError();
