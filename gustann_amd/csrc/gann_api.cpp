@@ -7,7 +7,9 @@
 // place of the reference's exit()/abort()/throw.
 #include "../../include/gustann.h"
 
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <atomic>
@@ -95,9 +97,14 @@ struct PinnedBuf {
   ~PinnedBuf() {
     if (p) (void)hipHostFree(p);
   }
-  void alloc(size_t n) {
-    GANN_HIP(hipHostMalloc(&p, n ? n : 1, hipHostMallocMapped | hipHostMallocPortable));
+  void alloc(size_t n, unsigned extra_flags = 0) {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    GANN_HIP(hipHostMalloc(&p, n ? n : 1, hipHostMallocMapped | hipHostMallocPortable | extra_flags));
     bytes = n;
+  }
+  void ensure(size_t n, unsigned extra_flags = 0) {
+    if (!p || n > bytes) alloc(n, extra_flags);
   }
 };
 
@@ -232,6 +239,8 @@ struct gann_handle {
   // pages: HBM copy or pinned host memory
   DevBuf pages_dev;
   PinnedBuf pages_host;
+  std::string index_path;          // page source of the page-fetch mode without host pages
+  PinnedBuf slots, state_host;     // page-fetch mode: one page per query, state readback
   gann::IndexDev ix{};
   // pivot graph
   bool has_nav = false;
@@ -279,6 +288,7 @@ void open_handle(const gann_config* cfg, gann_handle* h) {
 
   std::string err;
   const int64_t es = cfg->dtype == GANN_UINT8 ? 1 : 4;
+  h->index_path = cfg->index_file;
   if (!gann::parse_disk_meta(cfg->index_file, es, &h->layout, &err))
     raise(err.rfind("cannot open", 0) == 0 ? GANN_ERR_IO : GANN_ERR_FORMAT, err);
   const gann::DiskLayout& L = h->layout;
@@ -409,6 +419,101 @@ void run_entries(gann_handle* h, const float* q_dev, int32_t nq, int32_t* entrie
   }
 }
 
+// Copies page `page` of the index (0-based, after the header sector) to dst:
+// from the host page image when the handle has one, else from the file.
+struct PageSource {
+  const uint8_t* mem = nullptr;
+  int fd = -1;
+  ~PageSource() {
+    if (fd >= 0) ::close(fd);
+  }
+  void open_for(const gann_handle* h) {
+    mem = (const uint8_t*)h->pages_host.p;
+    if (!mem) {
+      fd = ::open(h->index_path.c_str(), O_RDONLY);
+      if (fd < 0) raise(GANN_ERR_IO, "cannot open " + h->index_path + " for page reads");
+    }
+  }
+  void read(int64_t page, uint8_t* dst) const {
+    if (mem) {
+      std::memcpy(dst, mem + page * gann::kSectorBytes, (size_t)gann::kSectorBytes);
+      return;
+    }
+    const off_t off = (off_t)((page + 1) * gann::kSectorBytes);
+    size_t got = 0;
+    while (got < (size_t)gann::kSectorBytes) {
+      const ssize_t r = ::pread(fd, dst + got, (size_t)gann::kSectorBytes - got, off + (off_t)got);
+      if (r <= 0) raise(GANN_ERR_IO, "short page read from " + path);
+      got += (size_t)r;
+    }
+  }
+  std::string path;
+};
+
+// Step-wise search with a page-fetch stage (the hybrid executor's round,
+// src/hyd_task_runner.cu:126-275, with MemLoaderSync, src/io/mem_io.cpp:11-44):
+// after each GPU round the host reads every query's next node, copies that
+// node's page into the query's 4096-byte slot of a pinned, device-mapped
+// buffer, and the next round reads the record from the slot.  The kernels
+// and therefore the results are those of GANN_MODE_STEPWISE.
+void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                        const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
+                        int32_t* nexp, int32_t* nadc, hipStream_t s) {
+  const gann::DiskLayout& Ly = h->layout;
+  h->luts.ensure((size_t)nq * h->pq.dev.M * gann::kNumPivots * 4);
+  h->lists.ensure((size_t)nq * L * 8);
+  const size_t sb = gann::step_state_bytes();
+  h->state.ensure((size_t)nq * sb);
+  h->counters.ensure(64);
+  h->slots.ensure((size_t)nq * gann::kSectorBytes, hipHostMallocCoherent);
+  h->state_host.ensure((size_t)nq * sb);
+  void* slots_dev = nullptr;
+  GANN_HIP(hipHostGetDevicePointer(&slots_dev, h->slots.p, 0));
+  PageSource src;
+  src.path = h->index_path;
+  src.open_for(h);
+  GANN_HIP(gann::launch_step_init(h->pq.dev, q_dev, nq, entries, h->luts.as<float>(), h->state.p, s));
+  int32_t* active = h->counters.as<int32_t>() + 1;
+  GANN_HIP(gann::launch_fill_i32(active, 1, nq, s));
+  const int nthreads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+  std::vector<int32_t> req((size_t)nq);
+  const int64_t max_rounds = Ly.num_pts + 2;
+  for (int64_t r = 0; r < max_rounds; ++r) {
+    GANN_HIP(hipMemcpyAsync(h->state_host.p, h->state.p, (size_t)nq * sb, hipMemcpyDeviceToHost, s));
+    GANN_HIP(hipStreamSynchronize(s));
+    int64_t n_active = 0;
+    for (int32_t j = 0; j < nq; ++j) {
+      req[(size_t)j] = gann::step_state_node(h->state_host.p, j);
+      if (req[(size_t)j] >= 0) {
+        if (req[(size_t)j] >= Ly.num_pts) raise(GANN_ERR_FORMAT, "request outside the index");
+        ++n_active;
+      }
+    }
+    if (n_active == 0) break;
+    // submit_task: page u / npp of every active query into its slot
+    std::vector<std::thread> pool;
+    std::atomic<int> failed{0};
+    for (int t = 0; t < nthreads; ++t)
+      pool.emplace_back([&, t] {
+        try {
+          for (int32_t j = t; j < nq; j += nthreads) {
+            const int32_t u = req[(size_t)j];
+            if (u >= 0)
+              src.read(u / Ly.nodes_per_page, (uint8_t*)h->slots.p + (size_t)j * gann::kSectorBytes);
+          }
+        } catch (...) {
+          failed = 1;
+        }
+      });
+    for (auto& th : pool) th.join();
+    if (failed) raise(GANN_ERR_IO, "page read failed for " + h->index_path);
+    GANN_HIP(gann::launch_step_round(h->ix, h->pq.dev, h->dtype, q_dev, nq, h->luts.as<float>(), topk,
+                                     L, h->lists.as<uint64_t>(), h->state.p, nns, dists, active,
+                                     (const uint8_t*)slots_dev, s));
+  }
+  GANN_HIP(gann::launch_step_finish(nq, topk, h->state.p, nns, dists, found, nexp, nadc, s));
+}
+
 void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                 int32_t mode, const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
                 int32_t* nexp, int32_t* nadc, hipStream_t s, int32_t beam = 1) {
@@ -449,6 +554,10 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
                                  dists, found, nexp, nadc, s));
     return;
   }
+  if (mode == GANN_MODE_STEPWISE_PAGED) {
+    run_stepwise_paged(h, q_dev, nq, topk, L, entries, nns, dists, found, nexp, nadc, s);
+    return;
+  }
   if (mode != GANN_MODE_STEPWISE) raise(GANN_ERR_INVALID, "unknown mode");
   // step-wise: LUTs in HBM, one launch per expansion round, host polls the
   // active count (the request[] round trip of src/hyd_task_runner.cu:126-178)
@@ -466,7 +575,7 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
     for (int k = 0; k < rounds_per_poll; ++k)
       GANN_HIP(gann::launch_step_round(h->ix, h->pq.dev, h->dtype, q_dev, nq, h->luts.as<float>(),
                                        topk, L, h->lists.as<uint64_t>(), h->state.p, nns, dists,
-                                       active, s));
+                                       active, nullptr, s));
     GANN_HIP(hipMemcpyAsync(host_active, active, 4, hipMemcpyDeviceToHost, s));
     GANN_HIP(hipStreamSynchronize(s));
     if (*host_active <= 0) break;

@@ -493,9 +493,9 @@ struct RecRegs {
   int deg_raw;
   uint32_t v;
   T x[kPer];
-  __device__ __forceinline__ void load(const IndexDev& ix, int64_t u) {
+  __device__ __forceinline__ void load(const IndexDev& ix, int64_t u) { load_at(ix, record_of(ix, u)); }
+  __device__ __forceinline__ void load_at(const IndexDev& ix, const uint8_t* rec) {
     const int lane = lane_id();
-    const uint8_t* rec = record_of(ix, u);
     deg_raw = *reinterpret_cast<const int32_t*>(rec + ix.data_len);
     const uint32_t* edge = reinterpret_cast<const uint32_t*>(rec + ix.data_len + 4);
     v = lane < ix.R ? edge[lane] : 0u;
@@ -959,6 +959,8 @@ __global__ __launch_bounds__(1024) void search_beam_kernel(IndexDev ix, PQDev pq
 // Per-query state of the step-wise form, kept in HBM between rounds
 // (the role of Data{visited_cnt,size} + request[] in src/impl/hyd.cuh:6-9,
 // src/impl/hyd_search_v2.cuh:35, :450-458).
+constexpr int64_t kStepSlotBytes = 4096;  // one index page per query slot
+
 struct StepState {
   int32_t u;      // node to expand this round, -1 when done
   int32_t sz;     // list size
@@ -996,7 +998,8 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
                                                         StepState* __restrict__ st,
                                                         int32_t* __restrict__ nns,
                                                         float* __restrict__ dists,
-                                                        int32_t* __restrict__ active) {
+                                                        int32_t* __restrict__ active,
+                                                        const uint8_t* __restrict__ slots) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int qi = blockIdx.x;
   if (qi >= nq) return;
@@ -1014,7 +1017,12 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
 
   const int32_t u = __builtin_amdgcn_readfirstlane(s.u);
   RecRegs<T, kMaxDimRegs> cur;
-  cur.load(ix, u);
+  // the record comes from the index pages, or from this query's 4096-byte
+  // slot that the host filled with u's page (src/hyd_task_runner.cu:216-240)
+  if (slots)
+    cur.load_at(ix, slots + (int64_t)qi * kStepSlotBytes + (u % ix.nodes_per_page) * ix.node_len);
+  else
+    cur.load(ix, u);
   float qv[kMaxDimRegs];
   restored_query_regs(q + (int64_t)qi * dim, pq.centroid, dim, qv);
   for (int i = lane; i < s.sz; i += kWave) A[i] = glist[i];
@@ -1172,12 +1180,13 @@ hipError_t launch_search_t(const IndexDev& ix, const PQDev& pq, const float* q, 
 template <typename T>
 hipError_t launch_round_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
                           const float* luts, int topk, int L, uint64_t* lists, StepState* st,
-                          int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
+                          int32_t* nns, float* dists, int32_t* active, const uint8_t* slots,
+                          hipStream_t stream) {
   const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + (size_t)L * 8 +
                       (size_t)list_scratch_words(L) * 4 + (size_t)topk * 8;
   return with_mw(pq.M, [&](auto mw) {
     hipLaunchKernelGGL((step_round_kernel<T, decltype(mw)::value>), dim3(nq), dim3(64), smem,
-                       stream, ix, pq, q, nq, luts, topk, L, lists, st, nns, dists, active);
+                       stream, ix, pq, q, nq, luts, topk, L, lists, st, nns, dists, active, slots);
     return hipGetLastError();
   });
 }
@@ -1263,6 +1272,9 @@ hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, co
 int max_beam_width() { return kMaxBeam; }
 
 size_t step_state_bytes() { return sizeof(StepState); }
+int32_t step_state_node(const void* host_states, int64_t i) {
+  return reinterpret_cast<const StepState*>(host_states)[i].u;
+}
 
 hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
                             float* luts, void* st, hipStream_t stream) {
@@ -1276,12 +1288,14 @@ hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32
 
 hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                              const float* luts, int topk, int L, uint64_t* lists, void* st,
-                             int32_t* nns, float* dists, int32_t* active, hipStream_t stream) {
+                             int32_t* nns, float* dists, int32_t* active, const uint8_t* slots,
+                             hipStream_t stream) {
   StepState* s = reinterpret_cast<StepState*>(st);
   if (dtype == 0)
     return launch_round_t<uint8_t>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active,
-                                   stream);
-  return launch_round_t<float>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, stream);
+                                   slots, stream);
+  return launch_round_t<float>(ix, pq, q, nq, luts, topk, L, lists, s, nns, dists, active, slots,
+                               stream);
 }
 
 hipError_t launch_step_finish(int nq, int topk, const void* st, int32_t* nns, float* dists,

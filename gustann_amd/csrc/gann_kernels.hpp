@@ -12,6 +12,9 @@ namespace gann {
 size_t search_smem_bytes(int M, int dim, int L, int R, int topk);
 size_t adc_smem_bytes(int M, int dim);
 size_t step_state_bytes();
+// The node query i expands next (-1: done), read from a host copy of the
+// step-wise state array.
+int32_t step_state_node(const void* host_states, int64_t i);
 
 hipError_t launch_pq_lut(const PQDev& pq, const float* q, int nq, float* lut_out,
                          hipStream_t stream);
@@ -41,7 +44,8 @@ hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32
                             float* luts, void* st, hipStream_t stream);
 hipError_t launch_step_round(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                              const float* luts, int topk, int L, uint64_t* lists, void* st,
-                             int32_t* nns, float* dists, int32_t* active, hipStream_t stream);
+                             int32_t* nns, float* dists, int32_t* active, const uint8_t* slots,
+                             hipStream_t stream);
 hipError_t launch_step_finish(int nq, int topk, const void* st, int32_t* nns, float* dists,
                               int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);

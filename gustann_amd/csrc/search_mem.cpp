@@ -5,7 +5,7 @@
 //
 //   search_mem --query Q --index I --pq_data P [--nav_graph N] --data_type uint8|float
 //              [--ground_truth GT] [--topk K] --ef_search L [L ...] [-R n] [-G]
-//              [--mode fused|lut|stepwise] [--device d] [--result_path FILE]
+//              [--mode fused|lut|stepwise|paged] [--device d] [--result_path FILE]
 //
 // --result_path (an addition) writes the ids of the first L's run as a bin
 // file [nq x topk] int32, the input of check_recall.
@@ -47,7 +47,7 @@ void usage() {
                "Usage: search_mem --query FILE --index FILE --pq_data PREFIX --data_type uint8|float\n"
                "                  --ef_search L [L ...] [--ground_truth FILE] [--topk K]\n"
                "                  [--nav_graph DIR] [--repeat|-R N] [--use-gpu-mem|-G]\n"
-               "                  [--mode fused|lut|stepwise] [--device D] [--result_path FILE]\n");
+               "                  [--mode fused|lut|stepwise|paged] [--device D] [--result_path FILE]\n");
 }
 
 }  // namespace
@@ -99,6 +99,7 @@ int main(int argc, char** argv) {
   int mode = GANN_MODE_FUSED;
   if (mode_s == "lut") mode = GANN_MODE_FUSED_LUT;
   else if (mode_s == "stepwise") mode = GANN_MODE_STEPWISE;
+  else if (mode_s == "paged") mode = GANN_MODE_STEPWISE_PAGED;
   else if (mode_s != "fused") die("unknown --mode " + mode_s);
   if (ef.empty()) die("--ef_search needs at least one value");
   for (int L : ef)

@@ -46,6 +46,11 @@ extern "C" {
                                  shared-codebook kernel when the pivot table fits in LDS */
 #define GANN_MODE_STEPWISE 1  /* one launch per expansion round, list in HBM (src/impl/hyd_search_v2.cuh) */
 #define GANN_MODE_FUSED_LUT 2 /* the fused kernel with a per-query LUT in LDS, forced */
+#define GANN_MODE_STEPWISE_PAGED 3 /* step-wise with a page-fetch stage: each round the host copies
+                                      every query's next page into a pinned slot the kernel reads
+                                      (src/hyd_task_runner.cu:200-275, src/io/mem_io.cpp:11-44);
+                                      pages come from host memory (pinned placement) or the index
+                                      file */
 
 typedef struct gann_handle gann_handle;
 typedef struct gann_pq gann_pq;

@@ -39,7 +39,7 @@ def test_single_L_reports_recall(tiny_u8):
     assert len(preview) == 5
 
 
-@pytest.mark.parametrize("mode", ["fused", "lut", "stepwise"])
+@pytest.mark.parametrize("mode", ["fused", "lut", "stepwise", "paged"])
 def test_sweep_table(tiny_u8, mode):
     P = tiny_u8["paths"]
     out = _run(["--query", P["query"], "--index", P["index"], "--pq_data", P["pq"], "--data_type",

@@ -12,7 +12,8 @@ from _helpers import exact_pq, write_custom_index
 from test_search_semantics import random_graph
 
 import oracle as orc
-from gustann_amd import (FLOAT, MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, UINT8, GannError, GustANN,
+from gustann_amd import (FLOAT, MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED, UINT8,
+                         GannError, GustANN,
                          GustANNConfig, GustANNStats)
 from gustann_amd import index as gi
 
@@ -86,6 +87,19 @@ def test_stepwise_matches_fused_and_oracle(u8):
     _assert_same(got, (on, od, of), ne, oe)
 
 
+@pytest.mark.parametrize("pinned", [False, True])
+def test_paged_stepwise_matches_oracle(tiny_u8, pinned):
+    # pages come from the index file (HBM placement) or the pinned host image
+    g = _open(_paths(tiny_u8), pinned=pinned)
+    ix = orc.Index(*_paths(tiny_u8))
+    Q = _queries(tiny_u8)[:120]
+    ne = np.empty(Q.shape[0], np.int32)
+    got = g.search(Q, Q.shape[0], 10, 32, mode=MODE_STEPWISE_PAGED, n_exp=ne)
+    on, od, of, oe, _ = ix.search(Q, 10, 32, threads=8)
+    _assert_same(got, (on, od, of), ne, oe)
+    g.close()
+
+
 def test_medoid_entry_without_nav(tiny_u8):
     g = _open(_paths(tiny_u8), nav=False)
     ix = orc.Index(*_paths(tiny_u8)[:2])
@@ -123,6 +137,8 @@ def test_fused_search_matches_oracle_float(tiny_f32, L):
     _assert_same(got2, (on, od, of))
     got3 = g.search(Q, Q.shape[0], 10, L, mode=MODE_FUSED_LUT)
     _assert_same(got3, (on, od, of))
+    got4 = g.search(Q, Q.shape[0], 10, L, mode=MODE_STEPWISE_PAGED)
+    _assert_same(got4, (on, od, of))
     g.close()
 
 
@@ -140,7 +156,7 @@ def test_random_graphs_match_oracle(tmp_path, seed, R, L, topk, trained):
     ix = orc.Index(*paths[:2])
     Q = rng.integers(0, 256, (40, D)).astype(np.float32)
     on, od, of, oe, _ = ix.search(Q, topk, L)
-    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE):
+    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED):
         ne = np.empty(40, np.int32)
         got = g.search(Q, 40, topk, L, n_exp=ne, mode=mode)
         _assert_same(got, (on, od, of), ne, oe)
