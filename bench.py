@@ -162,10 +162,12 @@ def bench_search(args):
 
     u8 = args.dtype == "uint8"
     sigma = args.sigma if args.sigma > 0 else (12.0 if u8 else 0.05)
-    spec = gi.DatasetSpec(name=f"mix{args.n}x{args.dim}{'' if u8 else 'f'}", n=args.n, dim=args.dim,
-                          dtype=args.dtype, nclusters=args.nclusters, sigma=sigma, R=64,
-                          L_build=100, M=args.M, nq=args.nq_search, k=10, nav_n=args.nav_n,
-                          gt_nq=args.gt_nq)
+    K = args.topk
+    spec = gi.DatasetSpec(name=f"mix{args.n}x{args.dim}{'' if u8 else 'f'}"
+                               + (f"z{args.zipf}" if args.zipf > 0 else ""),
+                          n=args.n, dim=args.dim, dtype=args.dtype, nclusters=args.nclusters,
+                          sigma=sigma, R=64, L_build=100, M=args.M, nq=args.nq_search,
+                          k=max(10, K), nav_n=args.nav_n, gt_nq=args.gt_nq, zipf_s=args.zipf)
     out_dir = args.data_dir or os.path.join("/tmp", f"gann_{spec.name}_{args.nav_n}")
     meta_path = os.path.join(out_dir, "meta.json")
     if os.path.exists(meta_path):
@@ -185,8 +187,9 @@ def bench_search(args):
     nq = Qr.shape[0]
     q_dev = torch.from_numpy(Qr).to(dev)
     ent = torch.empty(nq, dtype=torch.int32, device=dev)
-    nns = torch.empty((nq, 10), dtype=torch.int32, device=dev)
-    dd = torch.empty((nq, 10), dtype=torch.float32, device=dev)
+    nns = torch.empty((nq, K), dtype=torch.int32, device=dev)
+    dd = torch.empty((nq, K), dtype=torch.float32, device=dev)
+    mode = {"fused": 0, "stepwise": 1, "lut": 2, "paged": 3}[args.mode]
     fc = torch.empty(nq, dtype=torch.int32, device=dev)
     ne = torch.empty(nq, dtype=torch.int32, device=dev)
     na = torch.empty(nq, dtype=torch.int32, device=dev)
@@ -194,8 +197,9 @@ def bench_search(args):
     rows = []
     for L in args.L:
         def step():
-            g.search_device(q_dev.data_ptr(), nq, 10, L, ent.data_ptr(), nns.data_ptr(), dd.data_ptr(),
-                            fc.data_ptr(), ne.data_ptr(), na.data_ptr(), stream.cuda_stream)
+            g.search_device(q_dev.data_ptr(), nq, K, L, ent.data_ptr(), nns.data_ptr(), dd.data_ptr(),
+                            fc.data_ptr(), ne.data_ptr(), na.data_ptr(), stream.cuda_stream,
+                            beam_width=args.beam, mode=mode)
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
@@ -207,13 +211,13 @@ def bench_search(args):
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / args.steps
         res = nns[: gt.shape[0]].cpu().numpy()
-        rec = recall_at_k(res, gt, 10)
+        rec = recall_at_k(res, gt, K)
         exps = int(ne.sum().item())
         adcs = int(na.sum().item())
         alg = exps * (D * s_el + 4) + adcs * (4 + M) + nq * (4 * D + 80)
         rows.append({"L": L, "ms": ms, "qps": nq / (ms / 1e3), "recall": rec,
                      "expansions_per_query": exps / nq, "alg_GBps": alg / (ms / 1e3) / 1e9})
-        log(f"[bench] L={L} {ms:.3f} ms qps={nq / (ms / 1e3):.0f} recall@10={rec:.4f}")
+        log(f"[bench] L={L} {ms:.3f} ms qps={nq / (ms / 1e3):.0f} recall@{K}={rec:.4f}")
     best = next((r for r in rows if r["recall"] >= 0.9), rows[-1])
     g.close()
     result = {
@@ -224,7 +228,11 @@ def bench_search(args):
         "data": ("synthetic uint8 Gaussian mixture" if u8 else
                  f"synthetic L2-normalised f32 Gaussian mixture (sigma {sigma})"),
         "config": {"workload": (f"in_memory_search_{args.n}x{D}_{'u8' if u8 else 'f32'}_M{M}"
-                                + ("" if args.placement == "hbm" else "_host_pinned")),
+                                + ("" if args.placement == "hbm" else "_host_pinned")
+                                + ("" if args.mode == "fused" else f"_{args.mode}")
+                                + ("" if args.beam == 1 else f"_beam{args.beam}")
+                                + ("" if K == 10 else f"_top{K}")
+                                + ("" if args.zipf <= 0 else f"_zipf{args.zipf}")),
                    "nq": nq, "L": best["L"], "L_sweep": rows},
         "roofline": {"bound": "hbm", "achieved": best["alg_GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": best["alg_GBps"] / HBM_PEAK_GBS, "traffic": None},
@@ -237,19 +245,24 @@ def bench_search(args):
         threads = min(16, os.cpu_count() or 1)
         n0 = min(256, Q.shape[0])
         t = time.perf_counter()
-        ix.search(Q[:n0], 10, best["L"], threads=threads)
+        def cpu_search(Qs):
+            if args.beam > 1:
+                return ix.search_beam(Qs, K, best["L"], args.beam, threads=threads)[:3]
+            return ix.search(Qs, K, best["L"], threads=threads)[:3]
+        cpu_search(Q[:n0])
         per_q = (time.perf_counter() - t) / n0
         n = int(min(Q.shape[0], max(n0, args.cpu_seconds / max(per_q, 1e-9))))
         t = time.perf_counter()
-        on, od, of, _, _ = ix.search(Q[:n], 10, best["L"], threads=threads)
+        on, od, of = cpu_search(Q[:n])
         dt = time.perf_counter() - t
         result["cpu_baseline"] = {"value": n / dt, "unit": "queries/s", "cores": threads,
                                   "kind": "port",
                                   "sample": f"first {n} queries at L={best['L']}: oracle/gann_oracle.c "
-                                            f"orc_search, {threads} threads, {dt:.1f} s"}
+                                            f"{'orc_search_beam' if args.beam > 1 else 'orc_search'}, "
+                                            f"{threads} threads, {dt:.1f} s"}
         g2 = GustANN(UINT8 if u8 else FLOAT)
         g2.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), True)
-        gn, gd, gf = g2.search(Q[:n], n, 10, best["L"])
+        gn, gd, gf = g2.search(Q[:n], n, K, best["L"], beam_width=args.beam)
         g2.close()
         result["parity_sample_bitexact"] = bool(np.array_equal(gn, on) and np.array_equal(gf, of)
                                                 and np.array_equal(gd.view(np.uint32), od.view(np.uint32)))
@@ -347,6 +360,10 @@ def main():
     ap.add_argument("--M", type=int, default=32)
     ap.add_argument("--sigma", type=float, default=0.0, help="0 = 12 (uint8) / 0.05 (float)")
     ap.add_argument("--placement", choices=["hbm", "pinned"], default="hbm")
+    ap.add_argument("--mode", choices=["fused", "stepwise", "lut", "paged"], default="fused")
+    ap.add_argument("--beam", type=int, default=1)
+    ap.add_argument("--topk", type=int, default=10)
+    ap.add_argument("--zipf", type=float, default=0.0, help="> 0: query clusters ~ Zipf(s)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (queries shard across "
