@@ -312,6 +312,46 @@ def bench_knn(args):
     return result
 
 
+def bench_gather(args):
+    """The ADC microbenchmark's memory access alone (gann_diag_gather_rows):
+    the same 100M x 32-byte codes and 10k x 4096 ids (same seeds as the adc
+    workload), every row read and folded, no LUT and no arithmetic.  Its time
+    is the ceiling of the ADC scan on this access pattern."""
+    import ctypes as C
+    import torch
+    from gustann_amd import _native as N
+
+    nq, M, S, N_ = args.nq, 32, args.ids_per_query, args.num_codes
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    codes = torch.randint(0, 256, (N_, M), dtype=torch.uint8, device=dev, generator=g)
+    ids = torch.randint(0, N_, (nq, S), dtype=torch.int32, device=dev, generator=g)
+    out = torch.empty((nq, S), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    lib = N.hip_lib()
+
+    def step():
+        N.check(lib.gann_diag_gather_rows(C.c_void_p(codes.data_ptr()), N_, M, C.c_void_p(ids.data_ptr()),
+                                          nq * S, C.c_void_p(out.data_ptr()), C.c_void_p(stream.cuda_stream)))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    rows = nq * S
+    return {"workload": "gather_rows_adc_pattern", "rows": rows, "row_bytes": M,
+            "ms_per_launch": ms, "rows_per_s": rows / (ms / 1e3),
+            "row_bytes_GBps": rows * M / (ms / 1e3) / 1e9,
+            "line_bytes_GBps": rows * 128 / (ms / 1e3) / 1e9}
+
+
 def bench_copy(args):
     """Calibration kernel for the HBM traffic counters: one device-to-device
     copy of a buffer of known size (reads and writes copy_bytes each)."""
@@ -339,7 +379,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["adc", "search", "copy", "knn"], default="adc")
+    ap.add_argument("--workload", choices=["adc", "search", "copy", "knn", "gather"], default="adc")
     ap.add_argument("--knn-k", type=int, default=100)
     ap.add_argument("--copy-bytes", type=int, default=1 << 31)
     ap.add_argument("--nq", type=int, default=10000)
@@ -377,7 +417,8 @@ def main():
     if args.workload == "copy":
         res = bench_copy(args)
     else:
-        res = {"adc": bench_adc, "search": bench_search, "knn": bench_knn}[args.workload](args)
+        res = {"adc": bench_adc, "search": bench_search, "knn": bench_knn,
+               "gather": bench_gather}[args.workload](args)
     print(json.dumps(res), flush=True)
 
 

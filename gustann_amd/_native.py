@@ -21,6 +21,7 @@ ABI_SYMBOLS = (
     "gann_search", "gann_search_ex", "gann_search_device", "gann_search_device_ex", "gann_nav_entry",
     "gann_pq_open", "gann_pq_create", "gann_pq_close", "gann_handle_pq",
     "gann_pq_lut_build", "gann_pq_adc_scan", "gann_pq_adc_scan_device", "gann_knn_exact",
+    "gann_diag_gather_rows",
 )
 
 
@@ -62,6 +63,7 @@ _SIGS = {
     "gann_search_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P,
                                  C.POINTER(Stats)]),
     "gann_search_device": (C.c_int, [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P]),
+    "gann_diag_gather_rows": (C.c_int, [_P, _I64, _I32, _P, _I64, _P, _P]),
     "gann_knn_exact": (C.c_int, [_P, _I64, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "gann_search_device_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P,
                                         _P, _P]),

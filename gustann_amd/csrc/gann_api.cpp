@@ -1008,4 +1008,18 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
   });
 }
 
+
+int gann_diag_gather_rows(const uint8_t* rows_dev, int64_t num_rows, int32_t row_bytes,
+                          const int32_t* ids_dev, int64_t n_ids, uint32_t* out_dev, void* stream) {
+  return guarded([&] {
+    if (row_bytes != 16 && row_bytes != 32 && row_bytes != 48 && row_bytes != 64)
+      raise(GANN_ERR_UNSUPPORTED, "row_bytes must be 16, 32, 48 or 64");
+    if (num_rows < 1 || n_ids < 0) raise(GANN_ERR_INVALID, "need num_rows >= 1 and n_ids >= 0");
+    if (n_ids == 0) return;
+    if (!rows_dev || !ids_dev || !out_dev) raise(GANN_ERR_INVALID, "NULL buffer");
+    GANN_HIP(gann::launch_gather_rows(rows_dev, num_rows, row_bytes, ids_dev, n_ids, out_dev,
+                                      (hipStream_t)stream));
+  });
+}
+
 }  // extern "C"

@@ -1087,6 +1087,42 @@ __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
+// ------------------------------------------------------------------ diagnostics
+
+// The ADC scan's memory access alone: every id's row of row_words 16-byte
+// words is read (plain vector loads, as CodeRow does) and folded to one word;
+// no LUT and no arithmetic.  Its time is the ceiling the ADC scan is measured
+// against.  Each thread keeps 8 ids in flight.  Ids outside [0, num_rows) read
+// row 0.
+template <int RW>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const u32x4* __restrict__ rows,
+                                                          int64_t num_rows,
+                                                          const int32_t* __restrict__ ids,
+                                                          int64_t n, uint32_t* __restrict__ out) {
+  constexpr int B = 8;
+  const int64_t base = ((int64_t)blockIdx.x * blockDim.x) * B + threadIdx.x;
+  int64_t id[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const int64_t s = base + (int64_t)b * blockDim.x;
+    const int32_t v = s < n ? ids[s] : 0;
+    id[b] = (v >= 0 && v < num_rows) ? v : 0;
+  }
+  u32x4 w[B][RW];
+#pragma unroll
+  for (int b = 0; b < B; ++b)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) w[b][r] = rows[id[b] * RW + r];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const int64_t s = base + (int64_t)b * blockDim.x;
+    uint32_t x = 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) x ^= w[b][r].x ^ w[b][r].y ^ w[b][r].z ^ w[b][r].w;
+    if (s < n) out[s] = x;
+  }
+}
+
 // ------------------------------------------------------------------ launchers
 
 namespace {
@@ -1270,6 +1306,30 @@ hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, co
 }
 
 int max_beam_width() { return kMaxBeam; }
+
+hipError_t launch_gather_rows(const uint8_t* rows, int64_t num_rows, int row_bytes,
+                              const int32_t* ids, int64_t n, uint32_t* out, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((n + 256 * 8 - 1) / (256 * 8)));
+  const u32x4* r = reinterpret_cast<const u32x4*>(rows);
+  switch (row_bytes) {
+    case 16:
+      hipLaunchKernelGGL(gather_rows_kernel<1>, grid, dim3(256), 0, stream, r, num_rows, ids, n, out);
+      break;
+    case 32:
+      hipLaunchKernelGGL(gather_rows_kernel<2>, grid, dim3(256), 0, stream, r, num_rows, ids, n, out);
+      break;
+    case 48:
+      hipLaunchKernelGGL(gather_rows_kernel<3>, grid, dim3(256), 0, stream, r, num_rows, ids, n, out);
+      break;
+    case 64:
+      hipLaunchKernelGGL(gather_rows_kernel<4>, grid, dim3(256), 0, stream, r, num_rows, ids, n, out);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 size_t step_state_bytes() { return sizeof(StepState); }
 int32_t step_state_node(const void* host_states, int64_t i) {

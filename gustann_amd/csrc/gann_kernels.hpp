@@ -12,6 +12,9 @@ namespace gann {
 size_t search_smem_bytes(int M, int dim, int L, int R, int topk);
 size_t adc_smem_bytes(int M, int dim);
 size_t step_state_bytes();
+// Diagnostic: the ADC scan's row reads alone (row_bytes 16, 32, 48 or 64).
+hipError_t launch_gather_rows(const uint8_t* rows, int64_t num_rows, int row_bytes,
+                              const int32_t* ids, int64_t n, uint32_t* out, hipStream_t stream);
 // The node query i expands next (-1: done), read from a host copy of the
 // step-wise state array.
 int32_t step_state_node(const void* host_states, int64_t i);

@@ -177,6 +177,17 @@ int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const i
 int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, const float* queries,
                    int32_t nq, int32_t k, int32_t device_id, int32_t* ids, float* dists);
 
+/* ---- diagnostics */
+
+/* The memory access of gann_pq_adc_scan_device alone: reads the row of every
+ * id (row_bytes of 16, 32, 48 or 64 at rows_dev + id * row_bytes, device
+ * memory, 16-byte aligned) with the same vector loads and folds it to one
+ * word in out_dev[i]; ids outside [0, num_rows) read row 0.  No counterpart
+ * in the reference: its time is the random-gather ceiling the ADC scan's
+ * roofline is read against.  Asynchronous on `stream`. */
+int gann_diag_gather_rows(const uint8_t* rows_dev, int64_t num_rows, int32_t row_bytes,
+                          const int32_t* ids_dev, int64_t n_ids, uint32_t* out_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
