@@ -14,6 +14,9 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -434,15 +437,19 @@ struct PageSource {
       if (fd < 0) raise(GANN_ERR_IO, "cannot open " + h->index_path + " for page reads");
     }
   }
-  void read(int64_t page, uint8_t* dst) const {
+  // Node u's record, into its place in the 4096-byte slot of its page (the
+  // loaders move whole pages; the kernel reads only the record, so only those
+  // bytes are copied).
+  void read_record(int64_t u, int64_t npp, int64_t node_len, uint8_t* slot) const {
+    const int64_t page = u / npp, off = (u % npp) * node_len;
     if (mem) {
-      std::memcpy(dst, mem + page * gann::kSectorBytes, (size_t)gann::kSectorBytes);
+      std::memcpy(slot + off, mem + page * gann::kSectorBytes + off, (size_t)node_len);
       return;
     }
-    const off_t off = (off_t)((page + 1) * gann::kSectorBytes);
+    const off_t pos = (off_t)((page + 1) * gann::kSectorBytes + off);
     size_t got = 0;
-    while (got < (size_t)gann::kSectorBytes) {
-      const ssize_t r = ::pread(fd, dst + got, (size_t)gann::kSectorBytes - got, off + (off_t)got);
+    while (got < (size_t)node_len) {
+      const ssize_t r = ::pread(fd, slot + off + got, (size_t)node_len - got, pos + (off_t)got);
       if (r <= 0) raise(GANN_ERR_IO, "short page read from " + path);
       got += (size_t)r;
     }
@@ -450,11 +457,68 @@ struct PageSource {
   std::string path;
 };
 
+// A fixed team of host threads that runs fn(t), t in [0, n), and waits; the
+// calling thread is member 0.
+class ThreadTeam {
+ public:
+  explicit ThreadTeam(int n) : n_(n) {
+    for (int t = 1; t < n; ++t) th_.emplace_back([this, t] { loop(t); });
+  }
+  ThreadTeam(const ThreadTeam&) = delete;
+  ThreadTeam& operator=(const ThreadTeam&) = delete;
+  ~ThreadTeam() {
+    {
+      std::lock_guard<std::mutex> g(m_);
+      stop_ = true;
+      ++gen_;
+    }
+    cv_.notify_all();
+    for (auto& t : th_) t.join();
+  }
+  void run(const std::function<void(int)>& fn) {
+    {
+      std::lock_guard<std::mutex> g(m_);
+      fn_ = &fn;
+      left_ = n_ - 1;
+      ++gen_;
+    }
+    cv_.notify_all();
+    fn(0);
+    std::unique_lock<std::mutex> l(m_);
+    done_.wait(l, [&] { return left_ == 0; });
+  }
+
+ private:
+  void loop(int t) {
+    int seen = 0;
+    for (;;) {
+      const std::function<void(int)>* f;
+      {
+        std::unique_lock<std::mutex> l(m_);
+        cv_.wait(l, [&] { return gen_ != seen; });
+        seen = gen_;
+        if (stop_) return;
+        f = fn_;
+      }
+      (*f)(t);
+      std::lock_guard<std::mutex> g(m_);
+      if (--left_ == 0) done_.notify_one();
+    }
+  }
+  int n_;
+  std::vector<std::thread> th_;
+  std::mutex m_;
+  std::condition_variable cv_, done_;
+  const std::function<void(int)>* fn_ = nullptr;
+  int left_ = 0, gen_ = 0;
+  bool stop_ = false;
+};
+
 // Step-wise search with a page-fetch stage (the hybrid executor's round,
 // src/hyd_task_runner.cu:126-275, with MemLoaderSync, src/io/mem_io.cpp:11-44):
 // after each GPU round the host reads every query's next node, copies that
-// node's page into the query's 4096-byte slot of a pinned, device-mapped
-// buffer, and the next round reads the record from the slot.  The kernels
+// node's record into its place in the query's 4096-byte page slot of a
+// pinned, device-mapped buffer, and the next round reads it from the slot.  The kernels
 // and therefore the results are those of GANN_MODE_STEPWISE.
 void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                         const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
@@ -476,6 +540,7 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
   int32_t* active = h->counters.as<int32_t>() + 1;
   GANN_HIP(gann::launch_fill_i32(active, 1, nq, s));
   const int nthreads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+  ThreadTeam team(nthreads);
   std::vector<int32_t> req((size_t)nq);
   const int64_t max_rounds = Ly.num_pts + 2;
   for (int64_t r = 0; r < max_rounds; ++r) {
@@ -490,22 +555,20 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
       }
     }
     if (n_active == 0) break;
-    // submit_task: page u / npp of every active query into its slot
-    std::vector<std::thread> pool;
+    // submit_task: every active query's record into its slot
     std::atomic<int> failed{0};
-    for (int t = 0; t < nthreads; ++t)
-      pool.emplace_back([&, t] {
-        try {
-          for (int32_t j = t; j < nq; j += nthreads) {
-            const int32_t u = req[(size_t)j];
-            if (u >= 0)
-              src.read(u / Ly.nodes_per_page, (uint8_t*)h->slots.p + (size_t)j * gann::kSectorBytes);
-          }
-        } catch (...) {
-          failed = 1;
+    team.run([&](int t) {
+      try {
+        for (int32_t j = t; j < nq; j += nthreads) {
+          const int32_t u = req[(size_t)j];
+          if (u >= 0)
+            src.read_record(u, Ly.nodes_per_page, Ly.node_len,
+                            (uint8_t*)h->slots.p + (size_t)j * gann::kSectorBytes);
         }
-      });
-    for (auto& th : pool) th.join();
+      } catch (...) {
+        failed = 1;
+      }
+    });
     if (failed) raise(GANN_ERR_IO, "page read failed for " + h->index_path);
     GANN_HIP(gann::launch_step_round(h->ix, h->pq.dev, h->dtype, q_dev, nq, h->luts.as<float>(), topk,
                                      L, h->lists.as<uint64_t>(), h->state.p, nns, dists, active,
