@@ -245,3 +245,32 @@ def test_search_device_matches_host_api(u8):
     hn, hd, hf = g.search(Q, nq, 10, 48)
     assert np.array_equal(nns.cpu().numpy(), hn) and np.array_equal(fc.cpu().numpy(), hf)
     assert np.array_equal(dd.cpu().numpy().view(np.uint32), hd.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_zero_degree_nodes_match_oracle(tmp_path, seed):
+    # records with degree 0 (including, for seed 12, possibly the entry):
+    # every mode, and the beam search, must agree with the oracle
+    rng = np.random.default_rng(seed)
+    n, D, R = 200, 16, 10
+    X = rng.integers(0, 256, (n, D)).astype(np.uint8)
+    adj = random_graph(rng, n, R, min_deg=0)
+    for u in rng.choice(n, 30, replace=False):
+        adj[int(u)] = []
+    medoid = int(rng.integers(0, n))
+    if seed == 12:
+        adj[medoid] = []
+    paths = write_custom_index(str(tmp_path), X, adj, medoid, R)
+    g = _open(paths, nav=False)
+    ix = orc.Index(*paths[:2])
+    Q = rng.integers(0, 256, (30, D)).astype(np.float32)
+    on, od, of, oe, _ = ix.search(Q, 5, 12)
+    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED):
+        ne = np.empty(30, np.int32)
+        got = g.search(Q, 30, 5, 12, n_exp=ne, mode=mode)
+        _assert_same(got, (on, od, of), ne, oe)
+    bn, bd, bf, be = ix.search_beam(Q, 5, 12, 3)
+    ne = np.empty(30, np.int32)
+    got = g.search(Q, 30, 5, 12, beam_width=3, n_exp=ne)
+    _assert_same(got, (bn, bd, bf), ne, be)
+    g.close()

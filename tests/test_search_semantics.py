@@ -60,14 +60,18 @@ def random_graph(rng, n, R, min_deg=1):
     return adj
 
 
-@pytest.mark.parametrize("seed,R,L,topk,trained", [(0, 12, 4, 3, False), (1, 12, 8, 5, False),
-                                                   (2, 12, 16, 10, True), (3, 8, 24, 10, True),
-                                                   (4, 16, 6, 6, False), (5, 10, 40, 20, True)])
-def test_oracle_search_matches_sort_restatement(tmp_path, seed, R, L, topk, trained):
+@pytest.mark.parametrize("seed,R,L,topk,trained,min_deg", [(0, 12, 4, 3, False, 1),
+                                                           (1, 12, 8, 5, False, 1),
+                                                           (2, 12, 16, 10, True, 1),
+                                                           (3, 8, 24, 10, True, 1),
+                                                           (4, 16, 6, 6, False, 1),
+                                                           (5, 10, 40, 20, True, 1),
+                                                           (6, 10, 12, 5, False, 0)])
+def test_oracle_search_matches_sort_restatement(tmp_path, seed, R, L, topk, trained, min_deg):
     rng = np.random.default_rng(seed)
     n, D = 240, 16
     X = rng.integers(0, 256, (n, D)).astype(np.uint8)
-    adj = random_graph(rng, n, R)
+    adj = random_graph(rng, n, R, min_deg=min_deg)
     pq = gi.train_pq(X, 4, sample=n, iters=4, seed=seed) if trained else exact_pq(X)
     idx, pqp, _ = write_custom_index(str(tmp_path), X, adj, 0, R, pq=pq)
     ix = orc.Index(idx, pqp)
