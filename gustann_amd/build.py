@@ -48,11 +48,13 @@ def build_hip(verbose=False):
     os.makedirs(LIB, exist_ok=True)
     objdir = os.path.join(ROOT, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
-    for src in ("gann_kernels.hip", "gann_knn.hip", "gann_api.cpp"):
-        obj = os.path.join(objdir, src.rsplit(".", 1)[0] + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
-        objs.append(obj)
+    from concurrent.futures import ThreadPoolExecutor
+    srcs = ("gann_kernels.hip", "gann_knn.hip", "gann_build.hip", "gann_api.cpp")
+    objs = [os.path.join(objdir, src.rsplit(".", 1)[0] + ".o") for src in srcs]
+    with ThreadPoolExecutor(max_workers=len(srcs)) as ex:
+        for f in [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+                  for src, obj in zip(srcs, objs)]:
+            f.result()
     out = os.path.join(LIB, "libgustann_hip.so")
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs,

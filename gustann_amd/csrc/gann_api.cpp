@@ -17,13 +17,17 @@
 #include <condition_variable>
 #include <functional>
 #include <mutex>
+#include <numeric>
+#include <random>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <string>
 #include <thread>
 #include <vector>
 
 #include "formats.hpp"
+#include "gann_build.hpp"
 #include "gann_kernels.hpp"
 #include "gann_knn.hpp"
 
@@ -1071,6 +1075,173 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
   });
 }
 
+
+namespace {
+
+// Device copy of [n][dim] uint8 rows padded to dp bytes, with squared norms.
+void upload_build_rows(const uint8_t* data, int64_t n, int dim, int dp, DevBuf& x, DevBuf& xn) {
+  x.ensure((size_t)n * dp);
+  xn.ensure((size_t)n * 4);
+  if (dp == dim) {
+    GANN_HIP(hipMemcpy(x.p, data, (size_t)n * dp, hipMemcpyHostToDevice));
+  } else {
+    GANN_HIP(hipMemset(x.p, 0, (size_t)n * dp));
+    GANN_HIP(hipMemcpy2D(x.p, (size_t)dp, data, (size_t)dim, (size_t)dim, (size_t)n, hipMemcpyHostToDevice));
+  }
+  GANN_HIP(gann::launch_build_norms(x.as<uint8_t>(), n, dp, xn.as<int32_t>(), 0));
+}
+
+int device_lds_limit(int device) {
+  int lim = 0;
+  GANN_HIP(hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+  return lim;
+}
+
+}  // namespace
+
+int gann_build_vamana(const uint8_t* data, int64_t n, int32_t dim, int32_t R, int32_t L, float alpha,
+                      uint64_t seed, int64_t max_batch, int32_t device_id, int32_t verbose,
+                      uint32_t* out_nbr, uint32_t* out_deg, int64_t* out_medoid) {
+  return guarded([&] {
+    if (!data || !out_nbr || !out_deg || !out_medoid) raise(GANN_ERR_INVALID, "NULL buffer");
+    if (n < 1 || n >= (int64_t)INT32_MAX) raise(GANN_ERR_INVALID, "need 1 <= n < 2^31 - 1");
+    const int dp = gann::build_row_bytes(dim);
+    if (dp == 0) raise(GANN_ERR_UNSUPPORTED, "dim must be in [1, 256]");
+    if (R < 1 || R > 64) raise(GANN_ERR_UNSUPPORTED, "R must be in [1, 64]");
+    if (L < 1 || L > 1024) raise(GANN_ERR_UNSUPPORTED, "L must be in [1, 1024]");
+    if (!std::isfinite(alpha) || !(alpha >= 1.0f)) raise(GANN_ERR_INVALID, "alpha must be finite and >= 1");
+    if (max_batch < 1) raise(GANN_ERR_INVALID, "max_batch must be >= 1");
+    const int64_t mb = std::min<int64_t>({max_batch, n, (int64_t)(INT32_MAX / 64)});
+    GANN_HIP(hipSetDevice(device_id));
+    int cus = 0;
+    GANN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_id));
+    const int lds = device_lds_limit(device_id);
+    if (gann::build_prune_waves(dp, (size_t)lds) < 1)
+      raise(GANN_ERR_UNSUPPORTED, "graph build: prune workspace exceeds the LDS limit");
+    check_lds(gann::build_search_smem_bytes(L, 4), device_id, "graph build search");
+    const auto t0 = std::chrono::steady_clock::now();
+    auto secs = [&] {
+      return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    };
+    DevBuf x, xn, nbr, deg, ord, sums, mean, best;
+    upload_build_rows(data, n, dim, dp, x, xn);
+    nbr.ensure((size_t)n * R * 4);
+    deg.ensure((size_t)n * 4);
+    // medoid: the point closest to the mean
+    sums.ensure((size_t)dp * 8);
+    GANN_HIP(hipMemset(sums.p, 0, (size_t)dp * 8));
+    GANN_HIP(gann::launch_build_col_sums(x.as<uint8_t>(), n, dp, sums.as<unsigned long long>(), 0));
+    std::vector<unsigned long long> hs((size_t)dp);
+    GANN_HIP(hipMemcpy(hs.data(), sums.p, (size_t)dp * 8, hipMemcpyDeviceToHost));
+    std::vector<float> hm((size_t)dim);
+    for (int j = 0; j < dim; ++j) hm[(size_t)j] = (float)((double)hs[(size_t)j] / (double)n);
+    mean.ensure((size_t)dim * 4);
+    GANN_HIP(hipMemcpy(mean.p, hm.data(), (size_t)dim * 4, hipMemcpyHostToDevice));
+    best.ensure(8);
+    GANN_HIP(hipMemset(best.p, 0xff, 8));
+    GANN_HIP(gann::launch_build_medoid(x.as<uint8_t>(), n, dim, dp, mean.as<float>(),
+                                       best.as<unsigned long long>(), 0));
+    unsigned long long hb = 0;
+    GANN_HIP(hipMemcpy(&hb, best.p, 8, hipMemcpyDeviceToHost));
+    const uint32_t medoid = (uint32_t)(hb & 0xffffffffull);
+    if ((int64_t)medoid >= n) raise(GANN_ERR_FORMAT, "graph build: medoid search failed");
+    // random initial graph and the insertion order
+    const int init_deg = (int)std::min<int64_t>(R / 2 > 0 ? R / 2 : 1, n - 1);
+    gann::BuildDev g{x.as<uint8_t>(), xn.as<int32_t>(), nbr.as<uint32_t>(), deg.as<uint32_t>(), n, dp, R};
+    GANN_HIP(gann::launch_build_random_graph(g, init_deg, seed, 0));
+    {
+      std::vector<uint32_t> order((size_t)n);
+      std::iota(order.begin(), order.end(), 0u);
+      std::mt19937_64 gen(seed ^ 0x5eedull);
+      std::shuffle(order.begin(), order.end(), gen);
+      ord.ensure((size_t)n * 4);
+      GANN_HIP(hipMemcpy(ord.p, order.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+    }
+    DevBuf pool_id, pool_d, pool_n, pa, pb, flags, seg, nseg, queue, temp;
+    pool_id.ensure((size_t)mb * gann::kBuildPoolMax * 4);
+    pool_d.ensure((size_t)mb * gann::kBuildPoolMax * 4);
+    pool_n.ensure((size_t)mb * 4);
+    pa.ensure((size_t)mb * R * 8);
+    pb.ensure((size_t)mb * R * 8);
+    flags.ensure((size_t)mb * R);
+    seg.ensure((size_t)mb * R * 4);
+    nseg.ensure(4);
+    queue.ensure(4);
+    size_t tb = 0;
+    GANN_HIP(gann::build_segments_temp_bytes(mb * R, &tb));
+    temp.ensure(tb);
+    if (verbose)
+      std::fprintf(stderr, "[gpu-vamana] n %lld dim %d R %d L %d alpha %.2f batch %lld: setup %.1f s\n",
+                   (long long)n, dim, R, L, (double)alpha, (long long)mb, secs());
+    double last = secs();
+    for (int pass = 0; pass < 2; ++pass) {
+      const float a = pass == 0 ? 1.0f : alpha;
+      int64_t off = 0, bs = pass == 0 ? 1 : mb;
+      while (off < n) {
+        const int64_t b = std::min(bs, n - off);
+        const uint32_t* pts = ord.as<uint32_t>() + off;
+        GANN_HIP(hipMemsetAsync(queue.p, 0, 4, 0));
+        GANN_HIP(gann::launch_build_search(g, pts, (int)b, medoid, L, pool_id.as<uint32_t>(), pool_d.as<float>(),
+                                           pool_n.as<int32_t>(), queue.as<int32_t>(), cus, 0));
+        GANN_HIP(hipMemsetAsync(queue.p, 0, 4, 0));
+        GANN_HIP(gann::launch_build_prune_fwd(g, pts, (int)b, pool_id.as<uint32_t>(), pool_d.as<float>(),
+                                              pool_n.as<int32_t>(), a, pa.as<unsigned long long>(),
+                                              queue.as<int32_t>(), cus, (size_t)lds, 0));
+        GANN_HIP(gann::launch_build_segments(temp.p, tb, pa.as<unsigned long long>(), pb.as<unsigned long long>(),
+                                             b * R, flags.as<uint8_t>(), seg.as<int32_t>(), nseg.as<int32_t>(), 0));
+        GANN_HIP(hipMemsetAsync(queue.p, 0, 4, 0));
+        GANN_HIP(gann::launch_build_reverse(g, pb.as<unsigned long long>(), b * R, seg.as<int32_t>(),
+                                            nseg.as<int32_t>(), a, queue.as<int32_t>(), cus, (size_t)lds, 0));
+        GANN_HIP(hipStreamSynchronize(0));
+        off += b;
+        if (pass == 0) bs = std::min(bs * 2, mb);
+        if (verbose && (secs() - last > 10.0 || off == n)) {
+          last = secs();
+          std::fprintf(stderr, "[gpu-vamana] alpha %.2f: %lld / %lld (%.1f s)\n", (double)a, (long long)off,
+                       (long long)n, last);
+        }
+      }
+    }
+    GANN_HIP(hipMemcpy(out_nbr, nbr.p, (size_t)n * R * 4, hipMemcpyDeviceToHost));
+    GANN_HIP(hipMemcpy(out_deg, deg.p, (size_t)n * 4, hipMemcpyDeviceToHost));
+    *out_medoid = (int64_t)medoid;
+  });
+}
+
+int gann_diag_robust_prune(const uint8_t* data, int64_t n, int32_t dim, int64_t p, const uint32_t* cand,
+                           int32_t ncand, float alpha, int32_t R, int32_t device_id, uint32_t* out,
+                           int32_t* nout) {
+  return guarded([&] {
+    if (!data || !out || !nout || (ncand > 0 && !cand)) raise(GANN_ERR_INVALID, "NULL buffer");
+    if (n < 1 || n >= (int64_t)INT32_MAX) raise(GANN_ERR_INVALID, "need 1 <= n < 2^31 - 1");
+    if (p < 0 || p >= n) raise(GANN_ERR_INVALID, "p outside [0, n)");
+    const int dp = gann::build_row_bytes(dim);
+    if (dp == 0) raise(GANN_ERR_UNSUPPORTED, "dim must be in [1, 256]");
+    if (R < 1 || R > 64) raise(GANN_ERR_UNSUPPORTED, "R must be in [1, 64]");
+    if (ncand < 0 || ncand > gann::kBuildCandMax) raise(GANN_ERR_UNSUPPORTED, "ncand must be in [0, 192]");
+    if (std::isnan(alpha)) raise(GANN_ERR_INVALID, "alpha is NaN");
+    for (int32_t i = 0; i < ncand; ++i)
+      if ((int64_t)cand[i] >= n) raise(GANN_ERR_INVALID, "candidate id outside [0, n)");
+    GANN_HIP(hipSetDevice(device_id));
+    const int lds = device_lds_limit(device_id);
+    DevBuf x, xn, nbr, deg, dc, dout, dn;
+    upload_build_rows(data, n, dim, dp, x, xn);
+    nbr.ensure((size_t)n * R * 4);
+    deg.ensure((size_t)n * 4);
+    dc.ensure((size_t)std::max(ncand, 1) * 4);
+    dout.ensure((size_t)R * 4);
+    dn.ensure(4);
+    if (ncand > 0) GANN_HIP(hipMemcpy(dc.p, cand, (size_t)ncand * 4, hipMemcpyHostToDevice));
+    gann::BuildDev g{x.as<uint8_t>(), xn.as<int32_t>(), nbr.as<uint32_t>(), deg.as<uint32_t>(), n, dp, R};
+    GANN_HIP(gann::launch_build_prune_one(g, (uint32_t)p, dc.as<uint32_t>(), ncand, alpha, dout.as<uint32_t>(),
+                                          dn.as<int32_t>(), (size_t)lds, 0));
+    int32_t k = 0;
+    GANN_HIP(hipMemcpy(&k, dn.p, 4, hipMemcpyDeviceToHost));
+    if (k < 0 || k > R) raise(GANN_ERR_FORMAT, "prune returned a bad count");
+    if (k > 0) GANN_HIP(hipMemcpy(out, dout.p, (size_t)k * 4, hipMemcpyDeviceToHost));
+    *nout = k;
+  });
+}
 
 int gann_diag_gather_rows(const uint8_t* rows_dev, int64_t num_rows, int32_t row_bytes,
                           const int32_t* ids_dev, int64_t n_ids, uint32_t* out_dev, void* stream) {

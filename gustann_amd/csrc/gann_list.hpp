@@ -1,0 +1,289 @@
+// Candidate-list update and top-k insertion shared by the search kernels
+// (gann_kernels.hip) and the graph builder (gann_build.hip): one wavefront
+// per query, list and scratch in LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <climits>
+
+#include "gann_device.hpp"
+
+namespace gann {
+
+// Per-expansion list update shared by the fused and the step-wise kernels.
+//
+// The reference (src/impl/pure_mem.cuh:350-419) merges the sorted new run
+// into the list by merge-path ranks, caps the result at 2L, removes every
+// entry whose id equals its predecessor's (a new copy always lands right
+// after its old copy, :358-360), caps at L and takes the first unvisited
+// entry below L.  The same list results from inserting only the new entries
+// that are not already present:
+//  * the 2L cap never changes the first L distinct entries (each id occurs
+//    at most twice among the first 2L merged entries), so it is dropped;
+//  * a new entry is a duplicate iff the old entry at its lower bound has the
+//    same id; the others move in at rank + (earlier inserted count);
+//  * an old entry i moves right by the number of inserted entries ranked at
+//    or before i;
+//  * every entry before the first unvisited one is visited, so the next
+//    node is min(new position of the old first-unvisited entry, position of
+//    the first inserted entry), tracked incrementally in fu.
+// The update runs in two phases so the caller can start fetching the next
+// node's record between them: plan() ranks the new run and picks the next
+// node without writing; apply() shifts the list in place (top chunk first,
+// skipping everything below the first insertion) and marks the node visited.
+// A: the list (sorted by key, distinct ids, visited flag in bit 31 of the low
+// word), capacity >= L; BM: list_scratch_words(L) words of scratch.
+
+// Scratch words per wave for the list update: a bitmap of the positions the
+// inserted entries take, two words per 64-entry chunk.
+__host__ __device__ constexpr int list_scratch_words(int L) { return 2 * ((L + kWave - 1) / kWave); }
+
+// Rank of `key` in the sorted list A[0..sz): the number of entries ordered
+// below it.  A first level shared by all lanes splits the list into 9
+// segments of s entries and reads the last entry of the first 8 (uniform
+// addresses); the entries below key are a prefix of those probes, so their
+// count fixes the lane's segment, which a branchless binary search with
+// uniform steps finishes.
+__device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key, bool active) {
+  if (!active) return 0;
+  int lo = 0, end = sz, span = sz;  // answer in [lo, end]; span bounds end - lo
+  if (sz > 8) {
+    const int s = (sz + 8) / 9;
+    int cnt = 0;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) cnt += A[min(s * (m + 1) - 1, sz - 1)] < key ? 1 : 0;
+    lo = min(s * cnt, sz);
+    end = cnt == 8 ? sz : min(s * (cnt + 1) - 1, sz - 1);
+    span = s;
+  }
+  for (int step = span > 0 ? 1 << (31 - __builtin_clz((unsigned)span)) : 0; step > 0; step >>= 1) {
+    const int p = lo + step - 1;
+    if (p < end && A[p] < key) lo += step;
+  }
+  return lo;
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+struct ListPlan {
+  uint64_t nkey;  // lanes 0..n_nd-1: the inserted entries, ascending; other lanes ~0
+  int p;          // lanes 0..n_nd-1: position of the lane's entry in the new list
+  int n_nd;       // inserted count (uniform)
+  int p0;         // position of the first inserted entry (uniform, INT_MAX if none)
+  int cand;       // position of the next node in the new list (uniform, -1: stop)
+  uint64_t sel;   // the selected entry (uniform)
+  int nsz;        // new list size (uniform)
+  int lb;         // every entry before lb is visited in the new list (uniform, <= nsz)
+};
+
+// Ranks each lane's candidate (lanes < deg) in the list, drops those whose id
+// is listed already, sorts the rest with their ranks into lanes 0..n_nd-1
+// (an inserted entry's position is then rank + lane) and picks the next node.
+__device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t key, int deg,
+                                              int sz, int fu) {
+  const int lane = lane_id();
+  const uint64_t fu_entry = fu < sz ? A[fu] : 0;
+  const bool active = lane < deg;
+  uint32_t r = (uint32_t)list_rank(A, sz, key, active);
+  // a candidate whose id is listed already sits at its lower bound
+  const bool dup = active && (int)r < sz && entry_id(A[r]) == entry_id(key);
+  if (!active || dup) key = ~(uint64_t)0;  // never a real key: ids are < 2^31 - 1
+  wave_sort64_kv(key, r);
+  ListPlan P;
+  P.nkey = key;
+  P.n_nd = __popcll(ballot64(key != ~(uint64_t)0));
+  P.p = (int)r + lane;
+  P.p0 = P.n_nd ? __builtin_amdgcn_readlane((int)r, 0) : INT_MAX;
+  P.nsz = min(sz + P.n_nd, L);
+  int fu_new = INT_MAX;
+  if (fu < sz) fu_new = fu + __popcll(ballot64(lane < P.n_nd && (int)r <= fu));
+  const int cand = min(fu_new, P.p0);
+  P.lb = min(cand, P.nsz);
+  if (cand >= P.nsz) {
+    P.cand = -1;
+    P.sel = 0;
+  } else {
+    P.cand = cand;
+    P.sel = cand == fu_new ? fu_entry : readlane64(key, 0);
+  }
+  return P;
+}
+
+// Applies the plan in place and returns the new first-unvisited index.  The
+// positions the inserted entries take are marked in the bitmap BM; output
+// position j then holds inserted entry nb(j) (nb = inserted entries placed
+// before j) if marked, else old entry j - nb(j).  Outputs are gathered in
+// batches of 8 chunks, top batch first: a batch reads only positions at or
+// above its lowest output minus 64 and writes after all its reads, so no
+// source is overwritten before it is read.
+// kSelect = false (beam search) only applies the insertions and returns P.lb.
+template <bool kSelect = true>
+__device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListPlan& P) {
+  constexpr int kBatch = 8;
+  const int lane = lane_id();
+  wave_sync();  // all reads of plan() done
+  const int start = min(P.p0, P.nsz);
+  if (start < P.nsz) {
+    const int ob_lo = (start / kWave) * kWave;
+    const int nch = (P.nsz - ob_lo + kWave - 1) / kWave;
+    const int w_lo = ob_lo / 32;
+    for (int w = lane; w < 2 * nch; w += kWave) BM[w_lo + w] = 0u;
+    wave_sync();
+    if (lane < P.n_nd && P.p < P.nsz) atomicOr(&BM[P.p >> 5], 1u << (P.p & 31));
+    wave_sync();
+    const uint32_t klo = (uint32_t)P.nkey, khi = (uint32_t)(P.nkey >> 32);
+    for (int b_hi = nch; b_hi > 0; b_hi -= kBatch) {
+      const int b_lo = max(0, b_hi - kBatch);
+      const uint32_t wv = lane < 2 * (b_hi - b_lo) ? BM[w_lo + 2 * b_lo + lane] : 0u;
+      uint64_t val[kBatch];
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        val[t] = 0;
+        if (b_lo + t < b_hi) {
+          const int ob = ob_lo + kWave * (b_lo + t);
+          uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * t + 1) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * t);
+          const int valid = P.nsz - ob;
+          if (valid < kWave) mo &= (1ull << valid) - 1;
+          const int nb = __popcll(ballot64(lane < P.n_nd && P.p < ob)) + rank_below(mo);
+          const bool isnew = (mo >> lane) & 1;
+          const int src = nb & (kWave - 1);
+          const uint32_t nlo = (uint32_t)__shfl((int)klo, src, kWave);
+          const uint32_t nhi = (uint32_t)__shfl((int)khi, src, kWave);
+          const int j = ob + lane;
+          uint64_t ov = 0;
+          if (!isnew && j < P.nsz) ov = A[j - nb];
+          val[t] = isnew ? (((uint64_t)nhi << 32) | nlo) : ov;
+        }
+      }
+      wave_sync();
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        const int j = ob_lo + kWave * (b_lo + t) + lane;
+        if (b_lo + t < b_hi && j < P.nsz) A[j] = val[t];
+      }
+      wave_sync();
+    }
+  }
+  if (!kSelect) return P.lb;
+  if (P.cand < 0) return P.nsz;
+  if (lane == 0) A[P.cand] = P.sel | kListVisited;
+  wave_sync();
+  int nfu = P.nsz;
+  for (int base = P.cand + 1; base < P.nsz; base += kWave) {
+    const int i = base + lane;
+    const uint64_t m = ballot64(i < P.nsz && !entry_visited(A[i]));
+    if (m) {
+      nfu = base + (int)__builtin_ctzll(m);
+      break;
+    }
+  }
+  return nfu;
+}
+
+// Top-k insertion of (d, id) into the sorted LDS list (src/impl/util.cuh:116-163):
+// the value lands after the last element that is not greater than it,
+// greater elements shift right, the list keeps at most k.
+__device__ __forceinline__ void topk_push(float* td, int32_t* ti, int* found, int k, float d,
+                                          int32_t id) {
+  const int lane = lane_id();
+  const int n = *found;
+  // position = 1 + index of the last element with !(elem > d)
+  int pos = 0;
+  for (int base = 0; base < n; base += kWave) {
+    const int j = base + lane;
+    const uint64_t ng = ballot64(j < n && !(td[j] > d));
+    if (ng) pos = base + 64 - (int)__builtin_clzll(ng);
+  }
+  // shift [pos, last) right by one, last chunk first; the element at index
+  // k-1 of a full list falls off
+  const int last = min(n, k - 1);
+  if (last > pos) {
+    for (int base = ((last - 1) / kWave) * kWave; base >= (pos / kWave) * kWave; base -= kWave) {
+      const int j = base + lane;
+      const bool mv = j >= pos && j < last;
+      float vd = 0.f;
+      int32_t vi = 0;
+      if (mv) {
+        vd = td[j];
+        vi = ti[j];
+      }
+      wave_sync();
+      if (mv) {
+        td[j + 1] = vd;
+        ti[j + 1] = vi;
+      }
+      wave_sync();
+    }
+  }
+  if (lane == 0 && pos < k) {
+    td[pos] = d;
+    ti[pos] = id;
+  }
+  if (n + 1 <= k) *found = n + 1;
+  wave_sync();
+}
+
+// The same insertion with the list in registers (k <= 64): lane j holds
+// element j and the shift is one DPP lane shift.
+__device__ __forceinline__ void topk_push_regs(float& td, int32_t& ti, int& found, int k, float d,
+                                               int32_t id) {
+  const int lane = lane_id();
+  const int n = found;
+  const uint64_t ng = ballot64(lane < n && !(td > d));
+  const int pos = ng ? 64 - (int)__builtin_clzll(ng) : 0;
+  const int last = min(n, k - 1);
+  const float sd = __uint_as_float(lane_shr1(__float_as_uint(td)));
+  const int32_t si = (int32_t)lane_shr1((uint32_t)ti);
+  if (lane > pos && lane <= last) {
+    td = sd;
+    ti = si;
+  }
+  if (lane == pos && pos < k) {
+    td = d;
+    ti = id;
+  }
+  if (n + 1 <= k) found = n + 1;
+}
+
+// Top-k state of one query: registers for k <= 64, else the LDS arrays td/ti.
+struct TopK {
+  float* td;
+  int32_t* ti;
+  int k, found;
+  float rd;
+  int32_t ri;
+  __device__ __forceinline__ TopK(float* td_, int32_t* ti_, int k_)
+      : td(td_), ti(ti_), k(k_), found(0), rd(0.0f), ri(0) {}
+  __device__ __forceinline__ void push(float d, int32_t id) {
+    if (k <= kWave)
+      topk_push_regs(rd, ri, found, k, d, id);
+    else
+      topk_push(td, ti, &found, k, d, id);
+  }
+  // slots past found are 0, as in the reference's zero-initialised vectors
+  __device__ __forceinline__ void store(int32_t* nns, float* dists, int64_t qi) const {
+    const int lane = lane_id();
+    if (k <= kWave) {
+      if (lane < k) {
+        const bool ok = lane < found;
+        nns[qi * k + lane] = ok ? ri : 0;
+        dists[qi * k + lane] = ok ? rd : 0.0f;
+      }
+    } else {
+      for (int j = lane; j < k; j += kWave) {
+        const bool ok = j < found;
+        nns[qi * k + j] = ok ? ti[j] : 0;
+        dists[qi * k + j] = ok ? td[j] : 0.0f;
+      }
+    }
+  }
+};
+
+}  // namespace gann

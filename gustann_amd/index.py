@@ -137,6 +137,40 @@ def brute_force_knn_gpu(X: np.ndarray, Q: np.ndarray, k: int, device_id: int = 0
     return ids, d
 
 
+def build_vamana_gpu(X: np.ndarray, R: int, L: int, alpha=1.2, seed=1, max_batch: int | None = None,
+                     device_id: int = 0, verbose=False):
+    """Vamana graph of uint8 points built on the GPU (gann_build_vamana):
+    the host builder's steps with points inserted in batches of at most
+    max_batch (default 2% of n).  Returns (nbr [n,R] u32, deg [n] u32, medoid)."""
+    import ctypes
+    from . import _native as N
+    X = np.ascontiguousarray(X)
+    if X.dtype != np.uint8:
+        raise ValueError("the GPU graph builder takes uint8 points")
+    n, dim = X.shape
+    if max_batch is None:
+        max_batch = max(64, -(-n // 50))
+    nbr = np.zeros((n, R), np.uint32)
+    deg = np.zeros(n, np.uint32)
+    med = ctypes.c_int64(0)
+    N.check(N.hip_lib().gann_build_vamana(_ptr(X), n, dim, R, L, alpha, seed, max_batch, device_id,
+                                          1 if verbose else 0, _ptr(nbr), _ptr(deg), ctypes.byref(med)))
+    return nbr, deg, int(med.value)
+
+
+def robust_prune_gpu(X: np.ndarray, p: int, cand, alpha: float, R: int, device_id: int = 0) -> np.ndarray:
+    """One RobustPrune step of the GPU builder (gann_diag_robust_prune)."""
+    import ctypes
+    from . import _native as N
+    X = np.ascontiguousarray(X, np.uint8)
+    c = np.ascontiguousarray(cand, np.uint32)
+    out = np.zeros(R, np.uint32)
+    k = ctypes.c_int32(0)
+    N.check(N.hip_lib().gann_diag_robust_prune(_ptr(X), X.shape[0], X.shape[1], p, _ptr(c), c.shape[0],
+                                               alpha, R, device_id, _ptr(out), ctypes.byref(k)))
+    return out[:k.value].copy()
+
+
 # ------------------------------------------------------------------ writers
 
 def write_disk_index(path, X, nbr, deg, medoid):

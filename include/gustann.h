@@ -177,6 +177,25 @@ int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const i
 int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, const float* queries,
                    int32_t nq, int32_t k, int32_t device_id, int32_t* ids, float* dists);
 
+/* ---- graph construction */
+
+/* Vamana graph of uint8 points built on the GPU.  Replaces the external
+ * DiskANN build the reference runs before searching
+ * (scripts/build_diskann_index.sh:7 for the base graph,
+ * scripts/gen_pivot_graph.sh:13 for the pivot graph); no counterpart in the
+ * reference's own code.  Same steps as a sequential Vamana build: medoid
+ * start, random initial graph of R/2 edges per node, a pass with alpha = 1
+ * then one with `alpha`, each inserting every point in a seeded random order
+ * by greedy search (list L), RobustPrune and reverse edges; points are
+ * inserted in batches of at most max_batch (doubling from 1 in the first
+ * pass) that see the graph as of the batch start.  data: [n][dim] on the
+ * host; out_nbr [n][R] and out_deg [n] on the host (row i: the first
+ * out_deg[i] entries valid), *out_medoid the start node.  dim <= 256,
+ * R <= 64, L <= 1024, n < 2^31 - 1.  verbose: progress lines on stderr. */
+int gann_build_vamana(const uint8_t* data, int64_t n, int32_t dim, int32_t R, int32_t L, float alpha,
+                      uint64_t seed, int64_t max_batch, int32_t device_id, int32_t verbose,
+                      uint32_t* out_nbr, uint32_t* out_deg, int64_t* out_medoid);
+
 /* ---- diagnostics */
 
 /* The memory access of gann_pq_adc_scan_device alone: reads the row of every
@@ -187,6 +206,17 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
  * roofline is read against.  Asynchronous on `stream`. */
 int gann_diag_gather_rows(const uint8_t* rows_dev, int64_t num_rows, int32_t row_bytes,
                           const int32_t* ids_dev, int64_t n_ids, uint32_t* out_dev, void* stream);
+
+/* One RobustPrune of the graph builder on the device: point p of data
+ * ([n][dim] uint8, host) over the candidate ids cand[0..ncand) (host,
+ * ncand <= 192): candidates sorted by (exact squared L2 to p, id), repeated
+ * ids and p dropped, each kept candidate occludes a later one j when
+ * d(p, j) / d(kept, j) > alpha; at most R kept, in order, into out (host,
+ * R entries), their count into *nout.  No counterpart in the reference; it
+ * lets tests check the builder's pruning step exactly. */
+int gann_diag_robust_prune(const uint8_t* data, int64_t n, int32_t dim, int64_t p, const uint32_t* cand,
+                           int32_t ncand, float alpha, int32_t R, int32_t device_id, uint32_t* out,
+                           int32_t* nout);
 
 #ifdef __cplusplus
 }

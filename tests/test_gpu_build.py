@@ -1,0 +1,162 @@
+"""GPU graph builder (gann_build_vamana, gann_diag_robust_prune).
+
+The reference's graphs come from DiskANN, which is absent, so the builder
+has no reference output to match (parity unpinned against DiskANN).  What
+is checked:
+  * its RobustPrune step, exactly, against a restatement of the rule
+    (index_builder.cpp robust_prune: sort by (distance, id), drop repeats
+    and p, occlusion d(p, j) / d(kept, j) > alpha with float32 division) and
+    against hand-computed cases;
+  * the medoid, identical to the host builder's;
+  * graph invariants (degree <= R, no self loops, no repeated or
+    out-of-range ids) and determinism of the whole build;
+  * search recall over the GPU-built graph against the host-built graph on
+    the same data, PQ and queries.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from gustann_amd import UINT8, GustANN, GustANNConfig
+from gustann_amd import index as gi
+
+pytestmark = pytest.mark.gpu
+
+
+def _sqd(a, b):
+    d = a.astype(np.int64) - b.astype(np.int64)
+    return int((d * d).sum())
+
+
+def prune_ref(X, p, cand, alpha, R):
+    """RobustPrune restated from the rule, in float32 like the builders."""
+    alpha = np.float32(alpha)
+    dist = {int(c): np.float32(_sqd(X[p], X[int(c)])) for c in cand}
+    ids = sorted((c for c in dist if c != p), key=lambda c: (dist[c], c))
+    occl = [np.float32(0.0)] * len(ids)
+    out = []
+    for i, c in enumerate(ids):
+        if len(out) >= R:
+            break
+        if occl[i] > alpha:
+            continue
+        out.append(c)
+        for j in range(i + 1, len(ids)):
+            if occl[j] > alpha:
+                continue
+            djk = np.float32(_sqd(X[c], X[ids[j]]))
+            f = np.float32(np.inf) if djk == 0 else np.float32(dist[ids[j]] / djk)
+            if f > occl[j]:
+                occl[j] = f
+    return np.array(out, np.uint32)
+
+
+def test_prune_known_answers():
+    # p = 0 at the origin; 1, 2, 3 on the first axis at 1, 2, 3; 4 at 2 on the
+    # second axis; 5 a copy of 1.  Squared distances to p: 1, 4, 9, 4, 1.
+    X = np.zeros((6, 32), np.uint8)
+    X[1, 0], X[2, 0], X[3, 0], X[4, 1] = 1, 2, 3, 2
+    X[5] = X[1]
+    cand = [3, 2, 1, 4, 5, 0, 2]
+    # alpha 1: 1 kept; 5 (d(1,5) = 0), 2 (4/1) and 3 (9/4) occluded; 4 (4/5) kept
+    assert gi.robust_prune_gpu(X, 0, cand, 1.0, 8).tolist() == [1, 4]
+    # alpha 3: 3 (9/4 <= 3, then 9/13 from 4) survives, 2 (4/1) does not
+    assert gi.robust_prune_gpu(X, 0, cand, 3.0, 8).tolist() == [1, 4, 3]
+    assert gi.robust_prune_gpu(X, 0, cand, 3.0, 2).tolist() == [1, 4]
+    assert gi.robust_prune_gpu(X, 0, cand, 1.0, 1).tolist() == [1]
+    assert gi.robust_prune_gpu(X, 0, [0, 0], 1.0, 8).tolist() == []
+    assert gi.robust_prune_gpu(X, 0, [], 1.0, 8).tolist() == []
+    for a, r in ((1.0, 8), (3.0, 8), (3.0, 2), (1.0, 1)):
+        assert prune_ref(X, 0, cand, a, r).tolist() == gi.robust_prune_gpu(X, 0, cand, a, r).tolist()
+
+
+@pytest.mark.parametrize("dim,R,alpha,seed", [(32, 16, 1.0, 1), (100, 32, 1.2, 2), (128, 64, 1.2, 3),
+                                              (256, 64, 1.5, 4), (64, 8, 1.0, 5), (200, 48, 1.2, 6)])
+def test_prune_matches_restatement(dim, R, alpha, seed):
+    r = np.random.default_rng(seed)
+    X, _ = gi.gen_mixture_u8(3000, dim, 6, seed, seed + 100, threads=4)
+    X[10:20] = X[5]  # repeated points: zero distances
+    for trial in range(8):
+        p = int(r.integers(0, X.shape[0])) if trial else 5
+        # candidates mostly from p's neighbourhood, as after a search
+        d = ((X.astype(np.int64) - X[p].astype(np.int64)) ** 2).sum(1)
+        near = np.argsort(d, kind="stable")[:400]
+        nc = int(r.integers(0, 193)) if trial > 1 else 192
+        cand = r.choice(near, nc).astype(np.uint32)
+        if nc > 3:
+            cand[0], cand[1] = p, cand[2]
+        got = gi.robust_prune_gpu(X, p, cand, alpha, R)
+        ref = prune_ref(X, p, cand, alpha, R)
+        assert np.array_equal(got, ref), (trial, got, ref)
+
+
+@pytest.fixture(scope="module")
+def mix():
+    X, _ = gi.gen_mixture_u8(20000, 128, 100, 11, 12, threads=8)
+    Qb, _ = gi.gen_mixture_u8(300, 128, 100, 11, 13, threads=8)
+    return X, Qb.astype(np.float32)
+
+
+def _check_graph(nbr, deg, n, R):
+    assert nbr.shape == (n, R) and deg.shape == (n,)
+    assert deg.max() <= R and deg.min() >= 1
+    mask = np.arange(R)[None, :] < deg[:, None]
+    assert (nbr[mask] < n).all()
+    rows = np.repeat(np.arange(n, dtype=np.uint32), deg.astype(np.int64))
+    assert not (nbr[mask] == rows).any()
+    s = np.where(mask, nbr.astype(np.int64), -1 - np.arange(R)[None, :])
+    s.sort(axis=1)
+    assert not (s[:, 1:] == s[:, :-1]).any()
+
+
+def test_invariants_medoid_determinism(mix):
+    X = mix[0][:6000]
+    a = gi.build_vamana_gpu(X, 32, 48, 1.2, seed=5)
+    _check_graph(a[0], a[1], X.shape[0], 32)
+    _, _, cmed = gi.build_vamana(X, 32, 48, 1.2, 5, threads=8)
+    assert a[2] == cmed
+    b = gi.build_vamana_gpu(X, 32, 48, 1.2, seed=5)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]) and a[2] == b[2]
+    # batches of one point: the build is sequential
+    c = gi.build_vamana_gpu(X[:1500], 16, 32, 1.2, seed=5, max_batch=1)
+    _check_graph(c[0], c[1], 1500, 16)
+
+
+def test_odd_dims_and_tiny_sets():
+    r = np.random.default_rng(9)
+    for n, dim, R in ((1, 8, 4), (2, 8, 4), (40, 33, 64), (300, 130, 24), (500, 90, 16), (400, 256, 32)):
+        X = r.integers(0, 256, (n, dim), dtype=np.uint8)
+        nbr, deg, med = gi.build_vamana_gpu(X, R, 20, 1.2, seed=1)
+        assert 0 <= med < n
+        if n == 1:
+            assert deg.tolist() == [0] and med == 0
+            continue
+        _check_graph(nbr, deg, n, R)
+        _, _, cmed = gi.build_vamana(X, R, 20, 1.2, 1, threads=2)
+        assert med == cmed
+
+
+def _recall(X, Q, nbr, deg, med, pq, k, L, d):
+    os.makedirs(d, exist_ok=True)
+    gi.write_disk_index(os.path.join(d, "g_disk.index"), X, nbr, deg, med)
+    gi.write_pq(os.path.join(d, "pq"), pq)
+    g = GustANN(UINT8)
+    g.init_pure_mem(GustANNConfig(os.path.join(d, "g_disk.index"), os.path.join(d, "pq"), ""), True)
+    nns, _, _ = g.search(Q, Q.shape[0], k, L)
+    g.close()
+    gt, _ = gi.brute_force_knn_gpu(X, Q, k)
+    return np.mean([len(set(a) & set(b)) / k for a, b in zip(nns, gt)])
+
+
+def test_search_recall_matches_host_graph(mix, tmp_path):
+    X, Q = mix
+    pq = gi.train_pq(X, 32, 20000, 8, 2, threads=8)
+    g = gi.build_vamana_gpu(X, 32, 64, 1.2, seed=3)
+    c = gi.build_vamana(X, 32, 64, 1.2, 3, threads=8)
+    _check_graph(g[0], g[1], X.shape[0], 32)
+    for L in (16, 48, 160):
+        rg = _recall(X, Q, *g, pq, 10, L, str(tmp_path / "gpu"))
+        rc = _recall(X, Q, *c, pq, 10, L, str(tmp_path / "cpu"))
+        print(f"L={L}: recall@10 GPU-built {rg:.4f}, host-built {rc:.4f}")
+        assert rg >= rc - 0.02, (L, rg, rc)
