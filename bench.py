@@ -167,8 +167,12 @@ def bench_search(args):
                                + (f"z{args.zipf}" if args.zipf > 0 else ""),
                           n=args.n, dim=args.dim, dtype=args.dtype, nclusters=args.nclusters,
                           sigma=sigma, R=64, L_build=100, M=args.M, nq=args.nq_search,
-                          k=max(10, K), nav_n=args.nav_n, gt_nq=args.gt_nq, zipf_s=args.zipf)
-    out_dir = args.data_dir or os.path.join("/tmp", f"gann_{spec.name}_{args.nav_n}")
+                          k=max(10, K), nav_n=args.nav_n, gt_nq=args.gt_nq, zipf_s=args.zipf,
+                          builder=args.builder,
+                          extra_queries=[{"name": a, "nq": int(b), "zipf_s": float(c), "k": int(d),
+                                          "gt_nq": args.gt_nq}
+                                         for a, b, c, d in (x.split(":") for x in args.extra_query_set)])
+    out_dir = args.data_dir or os.path.join("/tmp", f"gann_{spec.name}_{args.nav_n}_{args.builder}")
     meta_path = os.path.join(out_dir, "meta.json")
     if os.path.exists(meta_path):
         meta = json.load(open(meta_path))
@@ -176,8 +180,11 @@ def bench_search(args):
         log(f"[bench] building {spec.name} under {out_dir}")
         meta = gi.build_dataset(spec, out_dir, verbose=True)
     P = meta["paths"]
-    Q = gi.read_vecs(P["query"], np.uint8 if u8 else np.float32).astype(np.float32)
-    gt = gi.read_vecs(P["gt"], np.int32)
+    qk = f"query_{args.query_set}" if args.query_set else "query"
+    if qk not in P:
+        raise SystemExit(f"query set {args.query_set!r} was not built with this index")
+    Q = gi.read_vecs(P[qk], np.uint8 if u8 else np.float32).astype(np.float32)
+    gt = gi.read_vecs(P[f"gt_{args.query_set}" if args.query_set else "gt"], np.int32)
     g = GustANN(UINT8 if u8 else FLOAT)
     g.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), args.placement == "hbm")
     D, M, s_el = args.dim, args.M, (1 if u8 else 4)
@@ -189,7 +196,7 @@ def bench_search(args):
     ent = torch.empty(nq, dtype=torch.int32, device=dev)
     nns = torch.empty((nq, K), dtype=torch.int32, device=dev)
     dd = torch.empty((nq, K), dtype=torch.float32, device=dev)
-    mode = {"fused": 0, "stepwise": 1, "lut": 2, "paged": 3}[args.mode]
+    mode = {"fused": 0, "stepwise": 1, "lut": 2, "paged": 3, "gp": 4}[args.mode]
     fc = torch.empty(nq, dtype=torch.int32, device=dev)
     ne = torch.empty(nq, dtype=torch.int32, device=dev)
     na = torch.empty(nq, dtype=torch.int32, device=dev)
@@ -212,14 +219,14 @@ def bench_search(args):
         ms = e0.elapsed_time(e1) / args.steps
         res = nns[: gt.shape[0]].cpu().numpy()
         rec = recall_at_k(res, gt, K)
+        rec10 = recall_at_k(res, gt, 10) if K > 10 else rec
         exps = int(ne.sum().item())
         adcs = int(na.sum().item())
         alg = exps * (D * s_el + 4) + adcs * (4 + M) + nq * (4 * D + 80)
-        rows.append({"L": L, "ms": ms, "qps": nq / (ms / 1e3), "recall": rec,
+        rows.append({"L": L, "ms": ms, "qps": nq / (ms / 1e3), "recall": rec, "recall_at_10": rec10,
                      "expansions_per_query": exps / nq, "alg_GBps": alg / (ms / 1e3) / 1e9})
         log(f"[bench] L={L} {ms:.3f} ms qps={nq / (ms / 1e3):.0f} recall@{K}={rec:.4f}")
     best = next((r for r in rows if r["recall"] >= 0.9), rows[-1])
-    g.close()
     result = {
         "metric": METRIC, "value": best["qps"], "unit": "queries/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": best["ms"],
@@ -232,8 +239,10 @@ def bench_search(args):
                                 + ("" if args.mode == "fused" else f"_{args.mode}")
                                 + ("" if args.beam == 1 else f"_beam{args.beam}")
                                 + ("" if K == 10 else f"_top{K}")
-                                + ("" if args.zipf <= 0 else f"_zipf{args.zipf}")),
-                   "nq": nq, "L": best["L"], "L_sweep": rows},
+                                + ("" if args.zipf <= 0 else f"_zipf{args.zipf}")
+                                + ("" if not args.query_set else f"_queries_{args.query_set}")),
+                   "nq": nq, "L": best["L"], "L_sweep": rows, "index_builder": args.builder,
+                   "index_build_s": meta.get("build_s")},
         "roofline": {"bound": "hbm", "achieved": best["alg_GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": best["alg_GBps"] / HBM_PEAK_GBS, "traffic": None},
     }
@@ -260,12 +269,10 @@ def bench_search(args):
                                   "sample": f"first {n} queries at L={best['L']}: oracle/gann_oracle.c "
                                             f"{'orc_search_beam' if args.beam > 1 else 'orc_search'}, "
                                             f"{threads} threads, {dt:.1f} s"}
-        g2 = GustANN(UINT8 if u8 else FLOAT)
-        g2.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), True)
-        gn, gd, gf = g2.search(Q[:n], n, K, best["L"], beam_width=args.beam)
-        g2.close()
+        gn, gd, gf = g.search(Q[:n], n, K, best["L"], beam_width=args.beam)
         result["parity_sample_bitexact"] = bool(np.array_equal(gn, on) and np.array_equal(gf, of)
                                                 and np.array_equal(gd.view(np.uint32), od.view(np.uint32)))
+    g.close()
     return result
 
 
@@ -400,10 +407,15 @@ def main():
     ap.add_argument("--M", type=int, default=32)
     ap.add_argument("--sigma", type=float, default=0.0, help="0 = 12 (uint8) / 0.05 (float)")
     ap.add_argument("--placement", choices=["hbm", "pinned"], default="hbm")
-    ap.add_argument("--mode", choices=["fused", "stepwise", "lut", "paged"], default="fused")
+    ap.add_argument("--mode", choices=["fused", "stepwise", "lut", "paged", "gp"], default="fused")
     ap.add_argument("--beam", type=int, default=1)
     ap.add_argument("--topk", type=int, default=10)
     ap.add_argument("--zipf", type=float, default=0.0, help="> 0: query clusters ~ Zipf(s)")
+    ap.add_argument("--builder", choices=["cpu", "gpu"], default="cpu",
+                    help="index construction: host Vamana, or the GPU builder (uint8)")
+    ap.add_argument("--extra-query-set", action="append", default=[],
+                    help="NAME:NQ:ZIPF_S:K -- another query set (and top-K ground truth) built with the index")
+    ap.add_argument("--query-set", default="", help="search with the extra query set NAME")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (queries shard across "

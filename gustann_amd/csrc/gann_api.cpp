@@ -176,7 +176,7 @@ struct gann_pq {
   int device = 0;
   hipStream_t stream = nullptr;
   gann::PQDev dev{};
-  DevBuf pivots, pivots_t, centroid, chunk_off, codes;
+  DevBuf pivots, pivots_t, centroid, chunk_off, codes, piv_cb;
   bool codes_borrowed = false;
   // scratch of the host-pointer entry points
   DevBuf q, ids, out;
@@ -196,6 +196,9 @@ struct gann_pq {
       for (int j = 0; j < dim; ++j) pt[(size_t)j * gann::kNumPivots + i] = pivots[(size_t)i * dim + j];
     upload(pivots_t, pt.data(), pt.size() * 4);
     upload(this->pivots, pivots, (size_t)gann::kNumPivots * dim * 4);
+    std::vector<uint8_t> cb(gann::search_cb_pivot_bytes(dim));
+    gann::search_cb_pivot_layout(pivots, dim, cb.data());
+    upload(piv_cb, cb.data(), cb.size());
     upload(centroid, c, (size_t)dim * 4);
     upload(chunk_off, off, (size_t)(M + 1) * 4);
     dev.dim = dim;
@@ -209,6 +212,7 @@ struct gann_pq {
     dev.pivots_t = pivots_t.as<float>();
     dev.centroid = centroid.as<float>();
     dev.chunk_off = chunk_off.as<int32_t>();
+    dev.piv_cb = piv_cb.as<uint8_t>();
   }
 };
 
@@ -585,33 +589,41 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
                 int32_t mode, const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
                 int32_t* nexp, int32_t* nadc, hipStream_t s, int32_t beam = 1) {
   const gann::DiskLayout& Ly = h->layout;
+  // Shared-codebook kernels: one workgroup per CU holding the pivot table and
+  // as many lists as fit; below kMinLdsWaves lists, the pivots are read
+  // through the caches and the LDS holds lists only.
+  constexpr int kMinLdsWaves = 8;
+  const int w_lds = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, false);
+  const int w_gp = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true);
   if (beam > 1) {
     // beam search: shared-codebook kernel only
-    if (mode != GANN_MODE_FUSED)
-      raise(GANN_ERR_UNSUPPORTED, "beam_width > 1 runs only in GANN_MODE_FUSED");
-    const int waves = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit);
-    if (waves < 1)
-      raise(GANN_ERR_UNSUPPORTED, "beam_width > 1 needs the pivot table and one list in LDS");
+    if (mode != GANN_MODE_FUSED && mode != GANN_MODE_FUSED_GP)
+      raise(GANN_ERR_UNSUPPORTED, "beam_width > 1 runs only in GANN_MODE_FUSED or GANN_MODE_FUSED_GP");
+    const bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
+    const int waves = gp ? w_gp : w_lds;
+    if (waves < 1) raise(GANN_ERR_UNSUPPORTED, "beam_width > 1 needs one list in LDS");
     h->counters.ensure(64);
     h->qs.ensure((size_t)nq * Ly.dim * 4);
     const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
     GANN_HIP(gann::launch_search_beam(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, beam,
                                       nns, dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
-                                      h->qs.as<float>(), waves, blocks, s));
+                                      h->qs.as<float>(), waves, blocks, gp, s));
     return;
   }
-  if (mode == GANN_MODE_FUSED) {
-    // one workgroup per CU holding the pivot table, as many waves as fit
-    const int waves = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit);
-    if (waves >= 2) {
+  if (mode == GANN_MODE_FUSED || mode == GANN_MODE_FUSED_GP) {
+    const bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
+    const int waves = gp ? w_gp : w_lds;
+    if (waves >= 1 && (gp || waves >= 2)) {
       h->counters.ensure(64);
       h->qs.ensure((size_t)nq * Ly.dim * 4);
       const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
       GANN_HIP(gann::launch_search_cb(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,
                                       dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
-                                      h->qs.as<float>(), waves, blocks, s));
+                                      h->qs.as<float>(), waves, blocks, gp, s));
       return;
     }
+    if (mode == GANN_MODE_FUSED_GP)
+      raise(GANN_ERR_UNSUPPORTED, "GANN_MODE_FUSED_GP: one list does not fit in LDS");
     mode = GANN_MODE_FUSED_LUT;
   }
   if (mode == GANN_MODE_FUSED_LUT) {

@@ -26,6 +26,7 @@ struct PQDev {
   const float* centroid;    // [dim]
   const int32_t* chunk_off; // [M + 1]
   const uint8_t* codes;     // [num_pts][M]
+  const uint8_t* piv_cb;    // pivot rows in the shared-codebook layout (cb_row), for reads through the caches
 };
 
 // Disk-index pages resident in HBM (or pinned host memory).

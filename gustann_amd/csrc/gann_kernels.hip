@@ -473,7 +473,10 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
   return dist;
 }
 
-template <typename T, int MW, int W>
+// kGP: the pivot table is read from pq.piv_cb (HBM, through the caches)
+// instead of a copy in LDS, which then holds only the per-wave lists: the
+// form for large L, where lists beside a 128 KB table leave few waves.
+template <typename T, int MW, int W, bool kGP>
 __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
                                                          const float* __restrict__ q, int nq,
                                                          const int32_t* __restrict__ entries,
@@ -487,17 +490,24 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
   const uint32_t rowb = 4u * (uint32_t)dim;
-  const uint8_t* piv = smem_raw;
-  // pivot table (whole workgroup), the only workgroup barrier
-  for (int idx = threadIdx.x; idx < kPivots * dim; idx += blockDim.x) {
-    const int c = idx / dim, i = idx - c * dim;
-    *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, rowb) + 4 * i) = pq.pivots[idx];
+  const uint8_t* piv;
+  size_t lists_at = 0;
+  if constexpr (kGP) {
+    piv = (const uint8_t*)((const __attribute__((address_space(1))) uint8_t*)pq.piv_cb);
+  } else {
+    piv = smem_raw;
+    lists_at = CbSmem::pivot_bytes(dim);
+    // pivot table (whole workgroup), the only workgroup barrier
+    for (int idx = threadIdx.x; idx < kPivots * dim; idx += blockDim.x) {
+      const int c = idx / dim, i = idx - c * dim;
+      *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, rowb) + 4 * i) = pq.pivots[idx];
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
-  uint8_t* wbase = smem_raw + CbSmem::pivot_bytes(dim) + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
+  uint8_t* wbase = smem_raw + lists_at + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
   uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
   uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
@@ -565,7 +575,7 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
 // search_cb_kernel; KP rerank coordinates per lane (dim <= 32 * KP).
 constexpr int kMaxBeam = 4;
 
-template <typename T, int MW, int W, int KP>
+template <typename T, int MW, int W, int KP, bool kGP>
 __global__ __launch_bounds__(1024) void search_beam_kernel(IndexDev ix, PQDev pq,
                                                            const float* __restrict__ q, int nq,
                                                            const int32_t* __restrict__ entries,
@@ -580,16 +590,23 @@ __global__ __launch_bounds__(1024) void search_beam_kernel(IndexDev ix, PQDev pq
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
   const uint32_t rowb = 4u * (uint32_t)dim;
-  const uint8_t* piv = smem_raw;
-  for (int idx = threadIdx.x; idx < kPivots * dim; idx += blockDim.x) {
-    const int c = idx / dim, i = idx - c * dim;
-    *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, rowb) + 4 * i) = pq.pivots[idx];
+  const uint8_t* piv;
+  size_t lists_at = 0;
+  if constexpr (kGP) {
+    piv = (const uint8_t*)((const __attribute__((address_space(1))) uint8_t*)pq.piv_cb);
+  } else {
+    piv = smem_raw;
+    lists_at = CbSmem::pivot_bytes(dim);
+    for (int idx = threadIdx.x; idx < kPivots * dim; idx += blockDim.x) {
+      const int c = idx / dim, i = idx - c * dim;
+      *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, rowb) + 4 * i) = pq.pivots[idx];
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
-  uint8_t* wbase = smem_raw + CbSmem::pivot_bytes(dim) + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
+  uint8_t* wbase = smem_raw + lists_at + (size_t)wave * CbSmem::wave_bytes(dim, L, topk);
   uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
   uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
@@ -965,17 +982,29 @@ hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const f
                                 stream);
 }
 
-int search_cb_waves(int dim, int L, int topk, size_t lds_limit) {
-  const size_t piv = CbSmem::pivot_bytes(dim), w = CbSmem::wave_bytes(dim, L, topk);
+int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots) {
+  const size_t piv = global_pivots ? 0 : CbSmem::pivot_bytes(dim), w = CbSmem::wave_bytes(dim, L, topk);
   if (piv + w > lds_limit) return 0;
   return (int)std::min<size_t>(16, (lds_limit - piv) / w);
+}
+
+size_t search_cb_pivot_bytes(int dim) { return CbSmem::pivot_bytes(dim); }
+
+void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out) {
+  const uint32_t rowb = 4u * (uint32_t)dim;
+  std::fill(out, out + CbSmem::pivot_bytes(dim), (uint8_t)0);
+  for (uint32_t c = 0; c < (uint32_t)kPivots; ++c)
+    std::copy(reinterpret_cast<const uint8_t*>(pivots + (size_t)c * dim),
+              reinterpret_cast<const uint8_t*>(pivots + (size_t)(c + 1) * dim), out + c * rowb + (c & 0xF0u));
 }
 
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                            float* qs_all, int waves, int blocks, hipStream_t stream) {
-  const size_t smem = CbSmem::pivot_bytes(ix.dim) + (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
+                            float* qs_all, int waves, int blocks, bool global_pivots, hipStream_t stream) {
+  if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
+  const size_t smem = (global_pivots ? 0 : CbSmem::pivot_bytes(ix.dim)) +
+                      (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
   hipError_t e = launch_fill_i32(queue, 1, 0, stream);
   if (e != hipSuccess) return e;
   const int64_t n = (int64_t)nq * ix.dim;
@@ -987,9 +1016,14 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
     using T = decltype(t);
     return with_mw(pq.M, [&](auto mw) {
       return with_w(pq.chunk_w, [&](auto w) {
-        hipLaunchKernelGGL((search_cb_kernel<T, decltype(mw)::value, decltype(w)::value>),
-                           dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries,
-                           topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+        if (global_pivots)
+          hipLaunchKernelGGL((search_cb_kernel<T, decltype(mw)::value, decltype(w)::value, true>),
+                             dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries,
+                             topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+        else
+          hipLaunchKernelGGL((search_cb_kernel<T, decltype(mw)::value, decltype(w)::value, false>),
+                             dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries,
+                             topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
         return hipGetLastError();
       });
     });
@@ -1002,9 +1036,11 @@ hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, co
                               const int32_t* entries, int topk, int L, int bw, int32_t* nns,
                               float* dists, int32_t* found, int32_t* n_exp, int32_t* n_adc,
                               int32_t* queue, float* qs_all, int waves, int blocks,
-                              hipStream_t stream) {
+                              bool global_pivots, hipStream_t stream) {
   if (bw < 2 || bw > kMaxBeam) return hipErrorInvalidValue;
-  const size_t smem = CbSmem::pivot_bytes(ix.dim) + (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
+  if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
+  const size_t smem = (global_pivots ? 0 : CbSmem::pivot_bytes(ix.dim)) +
+                      (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
   hipError_t e = launch_fill_i32(queue, 1, 0, stream);
   if (e != hipSuccess) return e;
   const int64_t n = (int64_t)nq * ix.dim;
@@ -1016,10 +1052,16 @@ hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, co
     using T = decltype(t);
     return with_mw(pq.M, [&](auto mw) {
       return with_w(pq.chunk_w, [&](auto w) {
-        hipLaunchKernelGGL(
-            (search_beam_kernel<T, decltype(mw)::value, decltype(w)::value, decltype(kp)::value>),
-            dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries, topk, L, bw,
-            nns, dists, found, n_exp, n_adc, queue, qs_all);
+        if (global_pivots)
+          hipLaunchKernelGGL(
+              (search_beam_kernel<T, decltype(mw)::value, decltype(w)::value, decltype(kp)::value, true>),
+              dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries, topk, L, bw,
+              nns, dists, found, n_exp, n_adc, queue, qs_all);
+        else
+          hipLaunchKernelGGL(
+              (search_beam_kernel<T, decltype(mw)::value, decltype(w)::value, decltype(kp)::value, false>),
+              dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries, topk, L, bw,
+              nns, dists, found, n_exp, n_adc, queue, qs_all);
         return hipGetLastError();
       });
     });

@@ -29,19 +29,24 @@ hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_
 hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                          const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                          int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
-// Shared-codebook search: waves per workgroup that fit the LDS (0 = does not fit).
-int search_cb_waves(int dim, int L, int topk, size_t lds_limit);
+// Shared-codebook search: waves per workgroup that fit the LDS (0 = does not
+// fit), with the pivot table in LDS or (global_pivots) read from pq.piv_cb.
+int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots = false);
+// Size and contents of pq.piv_cb: the pivots [256][dim] in the kernel's row layout.
+size_t search_cb_pivot_bytes(int dim);
+void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out);
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                            float* qs_all, int waves, int blocks, hipStream_t stream);
-// Beam search with beam width bw in [2, max_beam_width()] (same LDS layout and
-// launch shape as launch_search_cb).
+                            float* qs_all, int waves, int blocks, bool global_pivots,
+                            hipStream_t stream);
+// Beam search with beam width bw in [2, max_beam_width()] (same LDS layout,
+// pivot placement and launch shape as launch_search_cb).
 hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                               const int32_t* entries, int topk, int L, int bw, int32_t* nns,
                               float* dists, int32_t* found, int32_t* n_exp, int32_t* n_adc,
                               int32_t* queue, float* qs_all, int waves, int blocks,
-                              hipStream_t stream);
+                              bool global_pivots, hipStream_t stream);
 int max_beam_width();
 hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,
                             float* luts, void* st, hipStream_t stream);

@@ -141,7 +141,8 @@ def build_vamana_gpu(X: np.ndarray, R: int, L: int, alpha=1.2, seed=1, max_batch
                      device_id: int = 0, verbose=False):
     """Vamana graph of uint8 points built on the GPU (gann_build_vamana):
     the host builder's steps with points inserted in batches of at most
-    max_batch (default 2% of n).  Returns (nbr [n,R] u32, deg [n] u32, medoid)."""
+    max_batch (default 0.5% of n, where recall over the built graph matched
+    the host-built graph's at 10M points).  Returns (nbr [n,R] u32, deg [n] u32, medoid)."""
     import ctypes
     from . import _native as N
     X = np.ascontiguousarray(X)
@@ -149,7 +150,7 @@ def build_vamana_gpu(X: np.ndarray, R: int, L: int, alpha=1.2, seed=1, max_batch
         raise ValueError("the GPU graph builder takes uint8 points")
     n, dim = X.shape
     if max_batch is None:
-        max_batch = max(64, -(-n // 50))
+        max_batch = max(64, -(-n // 200))
     nbr = np.zeros((n, R), np.uint32)
     deg = np.zeros(n, np.uint32)
     med = ctypes.c_int64(0)
@@ -296,6 +297,9 @@ class DatasetSpec:
     zipf_s: float = 0.0           # > 0: query clusters ~ Zipf(s)
     gt_nq: int = 0                # ground truth for the first gt_nq queries (0 = all)
     seed: int = 1234
+    builder: str = "cpu"          # "cpu": host Vamana + host ground truth; "gpu": both on the GPU (uint8)
+    # more query sets over the same index: {"name", "nq", "zipf_s", "k", "gt_nq"}
+    extra_queries: list = field(default_factory=list)
     extra: dict = field(default_factory=dict)
 
 
@@ -324,7 +328,13 @@ def build_dataset(spec: DatasetSpec, out_dir: str, threads=None, verbose=False) 
         Qb = Q
     if verbose:
         print(f"[{spec.name}] data {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    nbr, deg, med = build_vamana(X, spec.R, spec.L_build, spec.alpha, s + 3, threads)
+    gpu = spec.builder == "gpu"
+    if gpu and spec.dtype != "uint8":
+        raise ValueError("the GPU graph builder takes uint8 data")
+    if gpu:
+        nbr, deg, med = build_vamana_gpu(X, spec.R, spec.L_build, spec.alpha, s + 3, verbose=verbose)
+    else:
+        nbr, deg, med = build_vamana(X, spec.R, spec.L_build, spec.alpha, s + 3, threads)
     if verbose:
         print(f"[{spec.name}] vamana {time.time() - t0:.1f}s (avg deg {deg.mean():.1f})", file=sys.stderr,
               flush=True)
@@ -332,7 +342,10 @@ def build_dataset(spec: DatasetSpec, out_dir: str, threads=None, verbose=False) 
     if verbose:
         print(f"[{spec.name}] pq {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     ngt = spec.gt_nq if spec.gt_nq > 0 else spec.nq
-    gt, gtd = brute_force_knn(X, Q[:ngt], max(spec.k, 10), threads)
+    if gpu:
+        gt, gtd = brute_force_knn_gpu(X, Q[:ngt], max(spec.k, 10))
+    else:
+        gt, gtd = brute_force_knn(X, Q[:ngt], max(spec.k, 10), threads)
     if verbose:
         print(f"[{spec.name}] gt {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     paths = {
@@ -343,16 +356,47 @@ def build_dataset(spec: DatasetSpec, out_dir: str, threads=None, verbose=False) 
         "gt": os.path.join(out_dir, "gt.ivecs"),
     }
     write_disk_index(paths["index"], X, nbr, deg, med)
+    avg_deg = float(deg.mean())
+    del nbr, deg
     write_pq(paths["pq"], pq)
     write_vecs(paths["query"], Qb)
     write_vecs(paths["gt"], gt)
+    for xi, xq in enumerate(spec.extra_queries):
+        nm = xq["name"]
+        zs = float(xq.get("zipf_s", 0.0))
+        xcl = zipf_clusters(int(xq["nq"]), spec.nclusters, zs, s + 17 + xi) if zs > 0 else None
+        if spec.dtype == "uint8":
+            xQb, _ = gen_mixture_u8(int(xq["nq"]), spec.dim, spec.nclusters, s, s + 19 + xi, spec.lo, spec.hi,
+                                    spec.sigma, clusters=xcl, threads=threads)
+            xQ = xQb.astype(np.float32)
+        else:
+            xQ, _ = gen_mixture_f32(int(xq["nq"]), spec.dim, spec.nclusters, s, s + 19 + xi, spec.sigma,
+                                    clusters=xcl, threads=threads)
+            xQb = xQ
+        xk = max(int(xq.get("k", 10)), 10)
+        xg = int(xq.get("gt_nq", 0)) or xQ.shape[0]
+        if gpu:
+            xgt, _ = brute_force_knn_gpu(X, xQ[:xg], xk)
+        else:
+            xgt, _ = brute_force_knn(X, xQ[:xg], xk, threads)
+        paths[f"query_{nm}"] = os.path.join(out_dir, f"query_{nm}." + ("bvecs" if spec.dtype == "uint8" else "fvecs"))
+        paths[f"gt_{nm}"] = os.path.join(out_dir, f"gt_{nm}.ivecs")
+        write_vecs(paths[f"query_{nm}"], xQb)
+        write_vecs(paths[f"gt_{nm}"], xgt)
+    if verbose:
+        print(f"[{spec.name}] written {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     if spec.nav_n > 0:
         ids = sample_ids(spec.n, spec.nav_n)
         Xs = np.ascontiguousarray(X[ids])
-        nn, nd, nmed = build_vamana(Xs, spec.nav_R, spec.nav_L, 1.2, s + 5, threads)
+        if gpu:
+            nn, nd, nmed = build_vamana_gpu(Xs, spec.nav_R, spec.nav_L, 1.2, s + 5)
+        else:
+            nn, nd, nmed = build_vamana(Xs, spec.nav_R, spec.nav_L, 1.2, s + 5, threads)
         write_nav(paths["nav"], Xs, nn, nd, nmed, ids)
+        if verbose:
+            print(f"[{spec.name}] pivot graph {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     meta = {"spec": asdict(spec), "paths": paths, "medoid": med,
-            "avg_degree": float(deg.mean()), "build_s": time.time() - t0,
+            "avg_degree": avg_deg, "build_s": time.time() - t0,
             "rng": "splitmix64-seeded xoshiro256** streams per point, Box-Muller normals"}
     with open(os.path.join(out_dir, "meta.json"), "w") as f:
         json.dump(meta, f, indent=1)

@@ -43,7 +43,9 @@ extern "C" {
 #define GANN_PLACEMENT_HOST_PINNED 1 /* search_mem without -G: pages read zero-copy from pinned host memory */
 
 #define GANN_MODE_FUSED 0     /* one kernel per search (src/impl/pure_mem.cuh:243-432); picks the
-                                 shared-codebook kernel when the pivot table fits in LDS */
+                                 shared-codebook kernel with the pivot table in LDS while at least
+                                 8 lists fit beside it, else the same kernel reading the pivot
+                                 table through the caches (GANN_MODE_FUSED_GP) */
 #define GANN_MODE_STEPWISE 1  /* one launch per expansion round, list in HBM (src/impl/hyd_search_v2.cuh) */
 #define GANN_MODE_FUSED_LUT 2 /* the fused kernel with a per-query LUT in LDS, forced */
 #define GANN_MODE_STEPWISE_PAGED 3 /* step-wise with a page-fetch stage: each round the host copies
@@ -51,6 +53,9 @@ extern "C" {
                                       (src/hyd_task_runner.cu:200-275, src/io/mem_io.cpp:11-44);
                                       pages come from host memory (pinned placement) or the index
                                       file */
+#define GANN_MODE_FUSED_GP 4  /* the shared-codebook fused kernel with the pivot table read from HBM
+                                 through the caches and only the lists in LDS, forced (more lists
+                                 per CU at large L) */
 
 typedef struct gann_handle gann_handle;
 typedef struct gann_pq gann_pq;
@@ -103,7 +108,7 @@ int gann_get_info(const gann_handle* h, gann_index_info* info);
  * (bin/search_disk.cpp:189-192).  beam_width 1 is the reference's one node
  * per iteration (results identical to the reference); 2..4 selects the beam
  * search of this library (the first beam_width unvisited entries are expanded
- * per round; GANN_MODE_FUSED only), which the reference does not have.
+ * per round; GANN_MODE_FUSED or GANN_MODE_FUSED_GP only), which the reference does not have.
  * st may be NULL. */
 int gann_search(gann_handle* h, const float* q, int32_t nq, int32_t topk, int32_t L,
                 int32_t beam_width, int32_t* nns, float* dists, int32_t* found_cnt,

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from gustann_amd import FLOAT, MODE_FUSED, MODE_STEPWISE, UINT8, GannError, GustANN, GustANNConfig
+from gustann_amd import FLOAT, MODE_FUSED, MODE_FUSED_GP, MODE_STEPWISE, UINT8, GannError, GustANN, GustANNConfig
 from gustann_amd import index as gi
 
 pytestmark = pytest.mark.gpu
@@ -21,9 +21,9 @@ def _open(meta, dtype):
     return g, ix
 
 
-def _check(g, ix, Q, topk, L, bw):
+def _check(g, ix, Q, topk, L, bw, mode=MODE_FUSED):
     ne = np.empty(Q.shape[0], np.int32)
-    nns, d, f = g.search(Q, Q.shape[0], topk, L, beam_width=bw, n_exp=ne)
+    nns, d, f = g.search(Q, Q.shape[0], topk, L, beam_width=bw, n_exp=ne, mode=mode)
     on, od, of, oe = ix.search_beam(Q, topk, L, bw, threads=8)
     assert np.array_equal(f, of)
     assert np.array_equal(nns, on)
@@ -45,6 +45,17 @@ def test_beam_u8(u8, bw, L):
     meta, g, ix = u8
     Q = gi.read_vecs(meta["paths"]["query"], np.uint8).astype(np.float32)
     _check(g, ix, Q, 10, L, bw)
+
+
+@pytest.mark.parametrize("bw,L", [(2, 40), (4, 100), (4, 800)])
+def test_beam_u8_pivots_through_caches(u8, bw, L):
+    # the pivot table read from HBM instead of LDS (forced, and chosen by
+    # GANN_MODE_FUSED itself at L = 800, where few lists fit beside the table)
+    meta, g, ix = u8
+    Q = gi.read_vecs(meta["paths"]["query"], np.uint8).astype(np.float32)
+    _check(g, ix, Q, 10, L, bw, mode=MODE_FUSED_GP)
+    if L == 800:
+        _check(g, ix, Q, 10, L, bw)
 
 
 def test_beam_topk100_lds_path(u8):

@@ -12,7 +12,7 @@ from _helpers import exact_pq, write_custom_index
 from test_search_semantics import random_graph
 
 import oracle as orc
-from gustann_amd import (FLOAT, MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED, UINT8,
+from gustann_amd import (FLOAT, MODE_FUSED, MODE_FUSED_GP, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED, UINT8,
                          GannError, GustANN,
                          GustANNConfig, GustANNStats)
 from gustann_amd import index as gi
@@ -61,7 +61,7 @@ def test_nav_entries_match_oracle(u8):
     assert np.array_equal(ent, [ix.entry(q)[0] for q in Q])
 
 
-@pytest.mark.parametrize("mode", [MODE_FUSED, MODE_FUSED_LUT])
+@pytest.mark.parametrize("mode", [MODE_FUSED, MODE_FUSED_LUT, MODE_FUSED_GP])
 @pytest.mark.parametrize("L,topk", [(10, 10), (16, 10), (40, 10), (100, 10), (64, 1), (200, 100),
                                     (700, 10)])
 def test_fused_search_matches_oracle_u8(u8, L, topk, mode):
@@ -139,6 +139,8 @@ def test_fused_search_matches_oracle_float(tiny_f32, L):
     _assert_same(got3, (on, od, of))
     got4 = g.search(Q, Q.shape[0], 10, L, mode=MODE_STEPWISE_PAGED)
     _assert_same(got4, (on, od, of))
+    got5 = g.search(Q, Q.shape[0], 10, L, mode=MODE_FUSED_GP)
+    _assert_same(got5, (on, od, of))
     g.close()
 
 
@@ -156,7 +158,7 @@ def test_random_graphs_match_oracle(tmp_path, seed, R, L, topk, trained):
     ix = orc.Index(*paths[:2])
     Q = rng.integers(0, 256, (40, D)).astype(np.float32)
     on, od, of, oe, _ = ix.search(Q, topk, L)
-    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED):
+    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_FUSED_GP, MODE_STEPWISE, MODE_STEPWISE_PAGED):
         ne = np.empty(40, np.int32)
         got = g.search(Q, 40, topk, L, n_exp=ne, mode=mode)
         _assert_same(got, (on, od, of), ne, oe)
@@ -265,7 +267,7 @@ def test_zero_degree_nodes_match_oracle(tmp_path, seed):
     ix = orc.Index(*paths[:2])
     Q = rng.integers(0, 256, (30, D)).astype(np.float32)
     on, od, of, oe, _ = ix.search(Q, 5, 12)
-    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED):
+    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_FUSED_GP, MODE_STEPWISE, MODE_STEPWISE_PAGED):
         ne = np.empty(30, np.int32)
         got = g.search(Q, 30, 5, 12, n_exp=ne, mode=mode)
         _assert_same(got, (on, od, of), ne, oe)
