@@ -21,7 +21,7 @@ ABI_SYMBOLS = (
     "gann_search", "gann_search_ex", "gann_search_device", "gann_search_device_ex", "gann_nav_entry",
     "gann_pq_open", "gann_pq_create", "gann_pq_close", "gann_handle_pq",
     "gann_pq_lut_build", "gann_pq_adc_scan", "gann_pq_adc_scan_device", "gann_knn_exact",
-    "gann_diag_gather_rows", "gann_build_vamana", "gann_diag_robust_prune",
+    "gann_diag_gather_rows", "gann_build_vamana", "gann_diag_robust_prune", "gann_pq_encode",
 )
 
 
@@ -67,6 +67,7 @@ _SIGS = {
     "gann_knn_exact": (C.c_int, [_P, _I64, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "gann_build_vamana": (C.c_int, [_P, _I64, _I32, _I32, _I32, C.c_float, C.c_uint64, _I64, _I32,
                                     _I32, _P, _P, C.POINTER(_I64)]),
+    "gann_pq_encode": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _I32, _I32, _P]),
     "gann_diag_robust_prune": (C.c_int, [_P, _I64, _I32, _I64, _P, _I32, C.c_float, _I32, _I32, _P,
                                          C.POINTER(_I32)]),
     "gann_search_device_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P,
@@ -141,6 +142,8 @@ _IDX_SIGS = {
                              _P, _P, C.POINTER(_I64)]),
     "gib_pq": (C.c_int, [_P, _I64, _I64, C.c_int, C.c_int, _I64, C.c_int, C.c_uint64, C.c_int,
                          _P, _P, _P, _P]),
+    "gib_pq_train": (C.c_int, [_P, _I64, _I64, C.c_int, C.c_int, _I64, C.c_int, C.c_uint64, C.c_int,
+                               _P, _P, _P]),
     "gib_sample_ids": (C.c_int, [_I64, _I64, _P]),
     "gib_brute_force": (C.c_int, [_P, _I64, _P, _I64, _I64, C.c_int, _I64, _P, _P, C.c_int]),
     "gib_write_disk_index": (C.c_int, [C.c_char_p, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),

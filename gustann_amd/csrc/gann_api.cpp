@@ -1220,6 +1220,41 @@ int gann_build_vamana(const uint8_t* data, int64_t n, int32_t dim, int32_t R, in
   });
 }
 
+int gann_pq_encode(const void* data, int64_t n, int32_t dim, int32_t dtype, const float* pivots,
+                   const float* centroid, const int32_t* chunk_offsets, int32_t M, int32_t device_id,
+                   uint8_t* codes) {
+  return guarded([&] {
+    if (dtype != GANN_UINT8 && dtype != GANN_FLOAT) raise(GANN_ERR_INVALID, "unknown data type");
+    if (n < 0 || dim < 1 || M < 1 || M > dim) raise(GANN_ERR_INVALID, "need n >= 0 and 1 <= M <= dim");
+    if (n == 0) return;
+    if (!data || !pivots || !centroid || !chunk_offsets || !codes) raise(GANN_ERR_INVALID, "NULL buffer");
+    if (chunk_offsets[0] != 0 || chunk_offsets[M] != dim)
+      raise(GANN_ERR_INVALID, "chunk offsets must tile [0, dim)");
+    for (int32_t m = 0; m < M; ++m) {
+      const int32_t w = chunk_offsets[m + 1] - chunk_offsets[m];
+      if (w < 0) raise(GANN_ERR_INVALID, "chunk offsets must not decrease");
+      if (w > gann::kPqEncodeMaxW) raise(GANN_ERR_UNSUPPORTED, "chunks of at most 16 dims");
+    }
+    GANN_HIP(hipSetDevice(device_id));
+    const size_t elem = dtype == GANN_UINT8 ? 1 : 4;
+    const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t)1 << 30) / ((int64_t)dim * elem)));
+    DevBuf dx, dp, dc, doff, dcodes;
+    dx.ensure((size_t)chunk * dim * elem);
+    dcodes.ensure((size_t)chunk * M);
+    upload(dp, pivots, (size_t)gann::kNumPivots * dim * 4);
+    upload(dc, centroid, (size_t)dim * 4);
+    upload(doff, chunk_offsets, (size_t)(M + 1) * 4);
+    for (int64_t off = 0; off < n; off += chunk) {
+      const int64_t cn = std::min(chunk, n - off);
+      GANN_HIP(hipMemcpy(dx.p, (const uint8_t*)data + (size_t)off * dim * elem, (size_t)cn * dim * elem,
+                         hipMemcpyHostToDevice));
+      GANN_HIP(gann::launch_pq_encode(dx.p, dtype == GANN_UINT8 ? 0 : 1, cn, dim, dp.as<float>(), dc.as<float>(),
+                                      doff.as<int32_t>(), M, dcodes.as<uint8_t>(), 0));
+      GANN_HIP(hipMemcpy(codes + (size_t)off * M, dcodes.p, (size_t)cn * M, hipMemcpyDeviceToHost));
+    }
+  });
+}
+
 int gann_diag_robust_prune(const uint8_t* data, int64_t n, int32_t dim, int64_t p, const uint32_t* cand,
                            int32_t ncand, float alpha, int32_t R, int32_t device_id, uint32_t* out,
                            int32_t* nout) {

@@ -498,6 +498,46 @@ __global__ __launch_bounds__(64) void prune_one_kernel(BuildDev g, uint32_t p, c
   if (lane == 0) *nout = kept;
 }
 
+// ------------------------------------------------------------------ PQ encoding
+
+// One thread per point: for every chunk, the first of the 256 pivots with
+// the smallest distance, accumulated as fma(t, t, d) over the chunk's dims
+// in order with t = (x - centroid) - pivot (index_builder.cpp pq_encode).
+// Pivot reads are wave-uniform.
+template <typename T>
+__global__ __launch_bounds__(256) void pq_encode_kernel(const T* __restrict__ x, int64_t n, int dim,
+                                                        const float* __restrict__ pivots,
+                                                        const float* __restrict__ centroid,
+                                                        const int32_t* __restrict__ off, int M,
+                                                        uint8_t* __restrict__ codes) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool ok = i < n;
+  const T* row = x + (ok ? i : 0) * dim;
+  for (int m = 0; m < M; ++m) {
+    const int lo = off[m], w = off[m + 1] - lo;
+    float xv[kPqEncodeMaxW];
+#pragma unroll
+    for (int j = 0; j < kPqEncodeMaxW; ++j) xv[j] = j < w ? (float)row[lo + j] - centroid[lo + j] : 0.0f;
+    float bd = INFINITY;
+    int bk = 0;
+    for (int k = 0; k < kPivots; ++k) {
+      const float* pk = pivots + (int64_t)k * dim + lo;
+      float d = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kPqEncodeMaxW; ++j)
+        if (j < w) {
+          const float t = xv[j] - pk[j];
+          d = fma_f(t, t, d);
+        }
+      if (d < bd) {
+        bd = d;
+        bk = k;
+      }
+    }
+    if (ok) codes[i * M + m] = (uint8_t)bk;
+  }
+}
+
 template <class F>
 hipError_t with_nc(int dp, F&& f) {
   switch (dp) {
@@ -629,6 +669,20 @@ hipError_t launch_build_reverse(BuildDev g, const unsigned long long* pairs, int
                        pairs, npairs, seg_start, n_seg, alpha, queue);
     return hipGetLastError();
   });
+}
+
+hipError_t launch_pq_encode(const void* x, int dtype, int64_t n, int dim, const float* pivots,
+                            const float* centroid, const int32_t* chunk_off, int M, uint8_t* codes,
+                            hipStream_t stream) {
+  if (n < 1) return hipSuccess;
+  const dim3 grid(grid_for(n, 256));
+  if (dtype == 0)
+    hipLaunchKernelGGL(pq_encode_kernel<uint8_t>, grid, dim3(256), 0, stream, (const uint8_t*)x, n, dim, pivots,
+                       centroid, chunk_off, M, codes);
+  else
+    hipLaunchKernelGGL(pq_encode_kernel<float>, grid, dim3(256), 0, stream, (const float*)x, n, dim, pivots,
+                       centroid, chunk_off, M, codes);
+  return hipGetLastError();
 }
 
 hipError_t launch_build_prune_one(BuildDev g, uint32_t p, const uint32_t* cand, int ncand, float alpha,

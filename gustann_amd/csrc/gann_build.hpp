@@ -75,6 +75,14 @@ hipError_t launch_build_reverse(BuildDev g, const unsigned long long* pairs, int
                                 const int32_t* seg_start, const int32_t* n_seg, float alpha,
                                 int32_t* queue, int cus, size_t lds_limit, hipStream_t stream);
 
+// PQ codes of n points ([n][dim], uint8 (dtype 0) or f32) with pivots
+// [256][dim], centroid [dim] and chunk offsets [M+1] on the device; chunks of
+// at most kPqEncodeMaxW dims.
+constexpr int kPqEncodeMaxW = 16;
+hipError_t launch_pq_encode(const void* x, int dtype, int64_t n, int dim, const float* pivots,
+                            const float* centroid, const int32_t* chunk_off, int M, uint8_t* codes,
+                            hipStream_t stream);
+
 // RobustPrune of point p over cand[0..ncand) on the device (diagnostic
 // entry): out[0..*nout).
 hipError_t launch_build_prune_one(BuildDev g, uint32_t p, const uint32_t* cand, int ncand, float alpha,

@@ -356,12 +356,28 @@ void pq_train(const Points& P, int M, int64_t sample, int iters, uint64_t seed, 
   auto val = [&](int64_t i, int64_t j) -> float {
     return P.dtype == 0 ? (float)((const uint8_t*)P.data)[i * D + j] : ((const float*)P.data)[i * D + j];
   };
-  // centroid = mean of all points
+  // centroid = mean of all points (uint8: exact integer sums, so the
+  // threads' partial sums give the same double as a sequential pass)
   pq.centroid.assign((size_t)D, 0.f);
   {
     std::vector<double> acc((size_t)D, 0.0);
-    for (int64_t i = 0; i < P.n; ++i)
-      for (int64_t j = 0; j < D; ++j) acc[(size_t)j] += val(i, j);
+    if (P.dtype == 0) {
+      std::vector<int64_t> tot((size_t)D, 0);
+#pragma omp parallel num_threads(nthreads)
+      {
+        std::vector<int64_t> part((size_t)D, 0);
+        const uint8_t* x = (const uint8_t*)P.data;
+#pragma omp for schedule(static)
+        for (int64_t i = 0; i < P.n; ++i)
+          for (int64_t j = 0; j < D; ++j) part[(size_t)j] += x[i * D + j];
+#pragma omp critical
+        for (int64_t j = 0; j < D; ++j) tot[(size_t)j] += part[(size_t)j];
+      }
+      for (int64_t j = 0; j < D; ++j) acc[(size_t)j] = (double)tot[(size_t)j];
+    } else {
+      for (int64_t i = 0; i < P.n; ++i)
+        for (int64_t j = 0; j < D; ++j) acc[(size_t)j] += val(i, j);
+    }
     for (int64_t j = 0; j < D; ++j) pq.centroid[(size_t)j] = (float)(acc[(size_t)j] / (double)P.n);
   }
   // training sample
@@ -432,6 +448,9 @@ void pq_train(const Points& P, int M, int64_t sample, int iters, uint64_t seed, 
   }
 }
 
+// Code of each chunk: the first pivot with the smallest distance, the
+// distance accumulated as fma(t, t, d) over the chunk's dims in order with
+// t = (x - centroid) - pivot, the operations of the search's LUT entry.
 void pq_encode(const Points& P, int nthreads, gann::PQHost& pq) {
   const int64_t D = P.dim;
   const int M = pq.num_chunks;
@@ -450,7 +469,7 @@ void pq_encode(const Points& P, int nthreads, gann::PQHost& pq) {
                                   : ((const float*)P.data)[i * D + j]) -
                     pq.centroid[(size_t)j];
           float t = x - pq.pivots[(size_t)(k * D + j)];
-          d += t * t;
+          d = std::fma(t, t, d);
         }
         if (d < bd) {
           bd = d;
@@ -586,6 +605,22 @@ int gib_vamana(const void* data, int64_t n, int64_t dim, int dtype, int64_t R, i
 
 // Product quantizer training + encoding.  pivots [256][dim], centroid [dim],
 // chunk_offsets [M+1], codes [n][M].
+// Product quantizer training only (pivots, centroid, chunk offsets).
+int gib_pq_train(const void* data, int64_t n, int64_t dim, int dtype, int M, int64_t sample, int iters,
+                 uint64_t seed, int nthreads, float* pivots, float* centroid, int32_t* chunk_offsets) {
+  if (M < 1 || M > dim) {
+    g_err = "pq: need 1 <= M <= dim";
+    return 1;
+  }
+  Points P{data, n, dim, dtype};
+  gann::PQHost pq;
+  pq_train(P, M, sample, iters, seed, nthreads, pq);
+  std::memcpy(pivots, pq.pivots.data(), sizeof(float) * pq.pivots.size());
+  std::memcpy(centroid, pq.centroid.data(), sizeof(float) * pq.centroid.size());
+  std::memcpy(chunk_offsets, pq.chunk_offsets.data(), sizeof(int32_t) * pq.chunk_offsets.size());
+  return 0;
+}
+
 int gib_pq(const void* data, int64_t n, int64_t dim, int dtype, int M, int64_t sample, int iters,
            uint64_t seed, int nthreads, float* pivots, float* centroid, int32_t* chunk_offsets,
            uint8_t* codes) {

@@ -87,7 +87,11 @@ class PQTables:
         return int(self.chunk_offsets.shape[0] - 1)
 
 
-def train_pq(X: np.ndarray, M: int, sample=100_000, iters=12, seed=2, threads=None) -> PQTables:
+def train_pq(X: np.ndarray, M: int, sample=100_000, iters=12, seed=2, threads=None,
+             encoder: str = "cpu") -> PQTables:
+    """k-means on a sample of X (host), then codes for every point on the
+    host (encoder "cpu") or the GPU (encoder "gpu", gann_pq_encode: the
+    same rule and arithmetic, so the same codes)."""
     X = np.ascontiguousarray(X)
     n, dim = X.shape
     dtype = U8 if X.dtype == np.uint8 else F32
@@ -95,9 +99,31 @@ def train_pq(X: np.ndarray, M: int, sample=100_000, iters=12, seed=2, threads=No
     cen = np.empty(dim, np.float32)
     off = np.empty(M + 1, np.int32)
     codes = np.empty((n, M), np.uint8)
-    icheck(index_lib().gib_pq(_ptr(X), n, dim, dtype, M, sample, iters, seed, _threads(threads),
-                              _ptr(piv), _ptr(cen), _ptr(off), _ptr(codes)))
+    if encoder == "gpu":
+        icheck(index_lib().gib_pq_train(_ptr(X), n, dim, dtype, M, sample, iters, seed, _threads(threads),
+                                        _ptr(piv), _ptr(cen), _ptr(off)))
+        codes = pq_encode_gpu(X, piv, cen, off)
+    else:
+        icheck(index_lib().gib_pq(_ptr(X), n, dim, dtype, M, sample, iters, seed, _threads(threads),
+                                  _ptr(piv), _ptr(cen), _ptr(off), _ptr(codes)))
     return PQTables(piv, cen, off, codes)
+
+
+def pq_encode_gpu(X: np.ndarray, pivots, centroid, chunk_offsets, device_id: int = 0) -> np.ndarray:
+    """PQ codes of X on the GPU (gann_pq_encode)."""
+    from . import _native as N
+    X = np.ascontiguousarray(X)
+    if X.dtype != np.uint8:
+        X = np.ascontiguousarray(X, np.float32)
+    n, dim = X.shape
+    piv = np.ascontiguousarray(pivots, np.float32)
+    cen = np.ascontiguousarray(centroid, np.float32)
+    off = np.ascontiguousarray(chunk_offsets, np.int32)
+    M = off.shape[0] - 1
+    codes = np.empty((n, M), np.uint8)
+    N.check(N.hip_lib().gann_pq_encode(_ptr(X), n, dim, N.UINT8 if X.dtype == np.uint8 else N.FLOAT,
+                                       _ptr(piv), _ptr(cen), _ptr(off), M, device_id, _ptr(codes)))
+    return codes
 
 
 def sample_ids(num_data: int, num_samp: int) -> np.ndarray:
@@ -338,7 +364,7 @@ def build_dataset(spec: DatasetSpec, out_dir: str, threads=None, verbose=False) 
     if verbose:
         print(f"[{spec.name}] vamana {time.time() - t0:.1f}s (avg deg {deg.mean():.1f})", file=sys.stderr,
               flush=True)
-    pq = train_pq(X, spec.M, spec.pq_sample, spec.pq_iters, s + 4, threads)
+    pq = train_pq(X, spec.M, spec.pq_sample, spec.pq_iters, s + 4, threads, encoder="gpu" if gpu else "cpu")
     if verbose:
         print(f"[{spec.name}] pq {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     ngt = spec.gt_nq if spec.gt_nq > 0 else spec.nq

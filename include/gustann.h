@@ -182,7 +182,22 @@ int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const i
 int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, const float* queries,
                    int32_t nq, int32_t k, int32_t device_id, int32_t* ids, float* dists);
 
-/* ---- graph construction */
+/* ---- index construction */
+
+/* PQ codes of n points on the GPU: for every chunk m, the first of the 256
+ * pivots with the smallest distance, accumulated as fma(t, t, d) over the
+ * chunk's dims in order with t = (x - centroid) - pivot -- the operations of
+ * a LUT entry (src/impl/pq.cuh:35-43), so a point's code is the argmin of the
+ * LUT the search would build for that point.  Replaces the encoding step of
+ * DiskANN's PQ build (external to the reference, scripts/build_diskann_index.sh:7);
+ * no counterpart in the reference's own code.  data [n][dim] on the host,
+ * GANN_UINT8 or GANN_FLOAT; pivots [256][dim], centroid [dim], chunk_offsets
+ * [M+1] (tiling [0, dim), chunks of at most 16 dims) and codes [n][M] on
+ * the host. */
+int gann_pq_encode(const void* data, int64_t n, int32_t dim, int32_t dtype, const float* pivots,
+                   const float* centroid, const int32_t* chunk_offsets, int32_t M, int32_t device_id,
+                   uint8_t* codes);
+
 
 /* Vamana graph of uint8 points built on the GPU.  Replaces the external
  * DiskANN build the reference runs before searching

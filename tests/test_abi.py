@@ -39,7 +39,7 @@ def test_version_and_null_argument_errors():
 
 def test_index_builder_library_loads():
     lib = N.index_lib()
-    for name in ("gib_vamana", "gib_pq", "gib_brute_force", "gib_write_disk_index",
+    for name in ("gib_vamana", "gib_pq", "gib_pq_train", "gib_brute_force", "gib_write_disk_index",
                  "gib_write_pq", "gib_write_nav", "gib_inspect", "gib_sample_ids"):
         assert hasattr(lib, name)
 

@@ -161,3 +161,31 @@ def test_pivot_sampler_matches_gen_small_file_rule():
     a = gi.sample_ids(10000, 500)
     b = gi.sample_ids(10000, 500)
     assert np.array_equal(a, b) and np.all(np.diff(a) > 0) and a.min() >= 0 and a.max() < 10000
+
+
+@pytest.mark.parametrize("dtype,dim,M", [("uint8", 8, 2), ("uint8", 10, 3), ("float", 6, 4)])
+def test_pq_encoder_rule(dtype, dim, M):
+    # the host encoder's code = first argmin over the 256 pivots of
+    # fma-accumulated ((x - centroid) - pivot)^2 in dim order, restated with
+    # exact float32 rounding; the GPU encoder (gann_pq_encode) is checked
+    # against the host encoder in tests/test_gpu_build.py
+    from _helpers import fma_f32
+    r = np.random.default_rng(dim)
+    X = (r.integers(0, 256, (40, dim), dtype=np.uint8) if dtype == "uint8"
+         else r.standard_normal((40, dim)).astype(np.float32))
+    pq = gi.train_pq(X, M, sample=40, iters=3, seed=1)
+    # a pivot equal to another makes the first one win
+    piv, cen, off = pq.pivots, pq.centroid, pq.chunk_offsets
+    for i in range(X.shape[0]):
+        for m in range(M):
+            lo, hi = int(off[m]), int(off[m + 1])
+            best, bk = np.float32(np.inf), 0
+            for k in range(256):
+                d = np.float32(0.0)
+                for j in range(lo, hi):
+                    x = np.float32(np.float32(X[i, j]) - cen[j])
+                    t = np.float32(x - piv[k, j])
+                    d = fma_f32(t, t, d)
+                if d < best:
+                    best, bk = d, k
+            assert pq.codes[i, m] == bk, (i, m)

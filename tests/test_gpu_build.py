@@ -160,3 +160,18 @@ def test_search_recall_matches_host_graph(mix, tmp_path):
         rc = _recall(X, Q, *c, pq, 10, L, str(tmp_path / "cpu"))
         print(f"L={L}: recall@10 GPU-built {rg:.4f}, host-built {rc:.4f}")
         assert rg >= rc - 0.02, (L, rg, rc)
+
+
+@pytest.mark.parametrize("dtype,dim,M", [("uint8", 128, 32), ("uint8", 100, 7), ("float", 96, 48),
+                                         ("float", 33, 5)])
+def test_pq_encode_gpu_matches_host(dtype, dim, M):
+    r = np.random.default_rng(dim + M)
+    if dtype == "uint8":
+        X, _ = gi.gen_mixture_u8(30000, dim, 50, 3, 4, threads=8)
+    else:
+        X = r.standard_normal((30000, dim)).astype(np.float32)
+    pq = gi.train_pq(X, M, 5000, 4, 9, threads=8)
+    got = gi.pq_encode_gpu(X, pq.pivots, pq.centroid, pq.chunk_offsets)
+    assert np.array_equal(got, pq.codes)
+    g = gi.train_pq(X, M, 5000, 4, 9, threads=8, encoder="gpu")
+    assert np.array_equal(g.codes, pq.codes) and np.array_equal(g.pivots, pq.pivots)
