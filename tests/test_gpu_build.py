@@ -175,3 +175,29 @@ def test_pq_encode_gpu_matches_host(dtype, dim, M):
     assert np.array_equal(got, pq.codes)
     g = gi.train_pq(X, M, 5000, 4, 9, threads=8, encoder="gpu")
     assert np.array_equal(g.codes, pq.codes) and np.array_equal(g.pivots, pq.pivots)
+
+
+def test_build_disk_index_cli_gpu(tmp_path):
+    from gustann_amd import build_disk_index as bdi
+    X, _ = gi.gen_mixture_u8(20000, 64, 40, 21, 22, threads=8)
+    Qb, _ = gi.gen_mixture_u8(200, 64, 40, 21, 23, threads=8)
+    for name, A in (("base.u8bin", X), ("q.u8bin", Qb)):
+        with open(str(tmp_path / name), "wb") as f:
+            np.array(A.shape, np.int32).tofile(f)
+            A.tofile(f)
+    pre = str(tmp_path / "idx")
+    assert bdi.main(["--data_type", "uint8", "--index_path_prefix", pre, "--data_path",
+                     str(tmp_path / "base.u8bin"), "-R", "32", "-L", "64", "--pq_chunks", "16",
+                     "--pivot_graph", str(tmp_path / "nav"), "--pivot_samples", "2000",
+                     "--query_path", str(tmp_path / "q.u8bin"), "--gt_path", str(tmp_path / "gt.ivecs"),
+                     "--gt_k", "10"]) == 0
+    import oracle as orc
+    g = GustANN(UINT8)
+    g.init_pure_mem(GustANNConfig(pre + "_disk.index", pre + "_pq", str(tmp_path / "nav")), True)
+    Q = Qb.astype(np.float32)
+    nns, d, f = g.search(Q, Q.shape[0], 10, 200)
+    g.close()
+    on, od, of, _, _ = orc.Index(pre + "_disk.index", pre + "_pq", str(tmp_path / "nav")).search(Q, 10, 200)
+    assert np.array_equal(nns, on) and np.array_equal(d.view(np.uint32), od.view(np.uint32))
+    gt = gi.read_vecs(str(tmp_path / "gt.ivecs"), np.int32)
+    assert np.mean([len(set(a) & set(b)) / 10 for a, b in zip(nns, gt)]) > 0.8
