@@ -196,7 +196,7 @@ def bench_search(args):
     ent = torch.empty(nq, dtype=torch.int32, device=dev)
     nns = torch.empty((nq, K), dtype=torch.int32, device=dev)
     dd = torch.empty((nq, K), dtype=torch.float32, device=dev)
-    mode = {"fused": 0, "stepwise": 1, "lut": 2, "paged": 3, "gp": 4}[args.mode]
+    mode = {"fused": 0, "stepwise": 1, "lut": 2, "paged": 3, "gp": 4, "uring": 5}[args.mode]
     fc = torch.empty(nq, dtype=torch.int32, device=dev)
     ne = torch.empty(nq, dtype=torch.int32, device=dev)
     na = torch.empty(nq, dtype=torch.int32, device=dev)
@@ -407,7 +407,7 @@ def main():
     ap.add_argument("--M", type=int, default=32)
     ap.add_argument("--sigma", type=float, default=0.0, help="0 = 12 (uint8) / 0.05 (float)")
     ap.add_argument("--placement", choices=["hbm", "pinned"], default="hbm")
-    ap.add_argument("--mode", choices=["fused", "stepwise", "lut", "paged", "gp"], default="fused")
+    ap.add_argument("--mode", choices=["fused", "stepwise", "lut", "paged", "gp", "uring"], default="fused")
     ap.add_argument("--beam", type=int, default=1)
     ap.add_argument("--topk", type=int, default=10)
     ap.add_argument("--zipf", type=float, default=0.0, help="> 0: query clusters ~ Zipf(s)")

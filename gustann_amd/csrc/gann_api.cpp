@@ -8,6 +8,9 @@
 #include "../../include/gustann.h"
 
 #include <fcntl.h>
+#include <linux/io_uring.h>
+#include <sys/mman.h>
+#include <sys/syscall.h>
 #include <hip/hip_runtime.h>
 #include <unistd.h>
 
@@ -465,6 +468,112 @@ struct PageSource {
   std::string path;
 };
 
+// Whole-page reads through io_uring, driven by its system calls (the ring
+// set-up and the submission / completion protocol of the io_uring ABI; the
+// role of src/io/io_uring.cpp's IoUringLoader, which uses liburing): page
+// reads of 4096 bytes at queue depth up to `depth`, all of a batch reaped
+// before read_pages returns.
+class UringReader {
+ public:
+  UringReader() = default;
+  UringReader(const UringReader&) = delete;
+  UringReader& operator=(const UringReader&) = delete;
+  ~UringReader() {
+    if (sqes_) ::munmap(sqes_, sqe_len_);
+    if (cq_map_ && cq_map_ != sq_map_) ::munmap(cq_map_, cq_len_);
+    if (sq_map_) ::munmap(sq_map_, sq_len_);
+    if (rfd_ >= 0) ::close(rfd_);
+  }
+  // false (errno set) when the kernel refuses io_uring
+  bool init(unsigned depth) {
+    io_uring_params p;
+    std::memset(&p, 0, sizeof p);
+    rfd_ = (int)::syscall(__NR_io_uring_setup, depth, &p);
+    if (rfd_ < 0) return false;
+    entries_ = p.sq_entries;
+    sq_len_ = p.sq_off.array + p.sq_entries * sizeof(unsigned);
+    cq_len_ = p.cq_off.cqes + p.cq_entries * sizeof(io_uring_cqe);
+    const bool single = (p.features & IORING_FEAT_SINGLE_MMAP) != 0;
+    if (single) sq_len_ = cq_len_ = std::max(sq_len_, cq_len_);
+    sq_map_ = map(sq_len_, IORING_OFF_SQ_RING);
+    cq_map_ = single ? sq_map_ : map(cq_len_, IORING_OFF_CQ_RING);
+    sqe_len_ = p.sq_entries * sizeof(io_uring_sqe);
+    sqes_ = (io_uring_sqe*)map(sqe_len_, IORING_OFF_SQES);
+    if (!sq_map_ || !cq_map_ || !sqes_) return false;
+    char* sq = (char*)sq_map_;
+    char* cq = (char*)cq_map_;
+    sq_head_ = (unsigned*)(sq + p.sq_off.head);
+    sq_tail_ = (unsigned*)(sq + p.sq_off.tail);
+    sq_mask_ = *(unsigned*)(sq + p.sq_off.ring_mask);
+    sq_array_ = (unsigned*)(sq + p.sq_off.array);
+    cq_head_ = (unsigned*)(cq + p.cq_off.head);
+    cq_tail_ = (unsigned*)(cq + p.cq_off.tail);
+    cq_mask_ = *(unsigned*)(cq + p.cq_off.ring_mask);
+    cqes_ = (io_uring_cqe*)(cq + p.cq_off.cqes);
+    return true;
+  }
+  // dst[i] <- the 4096 bytes at file offset off[i]; bytes past the end of
+  // the file read as zero.  Returns an error message, or "" on success.
+  std::string read_pages(int fd, const std::vector<std::pair<uint8_t*, off_t>>& reqs) {
+    const size_t n = reqs.size();
+    size_t next = 0, done = 0, inflight = 0;
+    std::string err;
+    while (done < n) {
+      unsigned tail = *sq_tail_;
+      const unsigned head = __atomic_load_n(sq_head_, __ATOMIC_ACQUIRE);
+      unsigned to_submit = 0;
+      while (next < n && inflight < entries_ && tail - head < entries_) {
+        const unsigned idx = tail & sq_mask_;
+        io_uring_sqe* e = &sqes_[idx];
+        std::memset(e, 0, sizeof *e);
+        e->opcode = IORING_OP_READ;
+        e->fd = fd;
+        e->addr = (uint64_t)(uintptr_t)reqs[next].first;
+        e->len = (uint32_t)gann::kSectorBytes;
+        e->off = (uint64_t)reqs[next].second;
+        e->user_data = (uint64_t)next;
+        sq_array_[idx] = idx;
+        ++tail;
+        ++next;
+        ++inflight;
+        ++to_submit;
+      }
+      __atomic_store_n(sq_tail_, tail, __ATOMIC_RELEASE);
+      const long r = ::syscall(__NR_io_uring_enter, rfd_, to_submit, 1u, IORING_ENTER_GETEVENTS, nullptr, 0);
+      if (r < 0 && errno != EINTR) return std::string("io_uring_enter: ") + std::strerror(errno);
+      unsigned ch = *cq_head_;
+      const unsigned ct = __atomic_load_n(cq_tail_, __ATOMIC_ACQUIRE);
+      for (; ch != ct; ++ch) {
+        const io_uring_cqe& c = cqes_[ch & cq_mask_];
+        const size_t i = (size_t)c.user_data;
+        if (c.res < 0) {
+          if (err.empty()) err = std::string("page read: ") + std::strerror(-c.res);
+        } else if (i < n && c.res < (int)gann::kSectorBytes) {
+          std::memset(reqs[i].first + c.res, 0, gann::kSectorBytes - (size_t)c.res);
+        }
+        ++done;
+        --inflight;
+      }
+      __atomic_store_n(cq_head_, ch, __ATOMIC_RELEASE);
+    }
+    return err;
+  }
+
+ private:
+  void* map(size_t len, off_t what) {
+    void* m = ::mmap(nullptr, len, PROT_READ | PROT_WRITE, MAP_SHARED | MAP_POPULATE, rfd_, what);
+    return m == MAP_FAILED ? nullptr : m;
+  }
+  int rfd_ = -1;
+  unsigned entries_ = 0, sq_mask_ = 0, cq_mask_ = 0;
+  void *sq_map_ = nullptr, *cq_map_ = nullptr;
+  size_t sq_len_ = 0, cq_len_ = 0, sqe_len_ = 0;
+  unsigned *sq_head_ = nullptr, *sq_tail_ = nullptr, *sq_array_ = nullptr;
+  unsigned *cq_head_ = nullptr, *cq_tail_ = nullptr;
+  io_uring_sqe* sqes_ = nullptr;
+  io_uring_cqe* cqes_ = nullptr;
+};
+
 // A fixed team of host threads that runs fn(t), t in [0, n), and waits; the
 // calling thread is member 0.
 class ThreadTeam {
@@ -530,7 +639,7 @@ class ThreadTeam {
 // and therefore the results are those of GANN_MODE_STEPWISE.
 void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                         const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
-                        int32_t* nexp, int32_t* nadc, hipStream_t s) {
+                        int32_t* nexp, int32_t* nadc, hipStream_t s, bool uring) {
   const gann::DiskLayout& Ly = h->layout;
   h->luts.ensure((size_t)nq * h->pq.dev.M * gann::kNumPivots * 4);
   h->lists.ensure((size_t)nq * L * 8);
@@ -543,7 +652,35 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
   GANN_HIP(hipHostGetDevicePointer(&slots_dev, h->slots.p, 0));
   PageSource src;
   src.path = h->index_path;
-  src.open_for(h);
+  // io_uring: whole pages from the index file, O_DIRECT where the file
+  // system takes it (the reference's loader opens with O_DIRECT)
+  UringReader ring;
+  int ufd = -1;
+  struct FdCloser {
+    int& fd;
+    ~FdCloser() {
+      if (fd >= 0) ::close(fd);
+    }
+  } ufd_closer{ufd};
+  std::vector<std::pair<uint8_t*, off_t>> reqs;
+  if (uring) {
+    ufd = ::open(h->index_path.c_str(), O_RDONLY | O_DIRECT);
+    if (ufd < 0) ufd = ::open(h->index_path.c_str(), O_RDONLY);
+    if (ufd < 0) raise(GANN_ERR_IO, "cannot open " + h->index_path + " for page reads");
+    if (!ring.init(4096))
+      raise(GANN_ERR_UNSUPPORTED, std::string("io_uring is not available: ") + std::strerror(errno));
+    // a file system that refuses O_DIRECT reads fails the first one: read
+    // through the page cache then
+    reqs.assign(1, {(uint8_t*)h->slots.p, (off_t)0});
+    if (!ring.read_pages(ufd, reqs).empty()) {
+      ::close(ufd);
+      ufd = ::open(h->index_path.c_str(), O_RDONLY);
+      if (ufd < 0) raise(GANN_ERR_IO, "cannot open " + h->index_path + " for page reads");
+    }
+    reqs.reserve((size_t)nq);
+  } else {
+    src.open_for(h);
+  }
   GANN_HIP(gann::launch_step_init(h->pq.dev, q_dev, nq, entries, h->luts.as<float>(), h->state.p, s));
   int32_t* active = h->counters.as<int32_t>() + 1;
   GANN_HIP(gann::launch_fill_i32(active, 1, nq, s));
@@ -563,7 +700,20 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
       }
     }
     if (n_active == 0) break;
-    // submit_task: every active query's record into its slot
+    // submit_task: every active query's page (io_uring) or record into its slot
+    if (uring) {
+      reqs.clear();
+      for (int32_t j = 0; j < nq; ++j)
+        if (req[(size_t)j] >= 0)
+          reqs.emplace_back((uint8_t*)h->slots.p + (size_t)j * gann::kSectorBytes,
+                            (off_t)((req[(size_t)j] / Ly.nodes_per_page + 1) * gann::kSectorBytes));
+      const std::string e = ring.read_pages(ufd, reqs);
+      if (!e.empty()) raise(GANN_ERR_IO, e + " (" + h->index_path + ")");
+      GANN_HIP(gann::launch_step_round(h->ix, h->pq.dev, h->dtype, q_dev, nq, h->luts.as<float>(), topk,
+                                       L, h->lists.as<uint64_t>(), h->state.p, nns, dists, active,
+                                       (const uint8_t*)slots_dev, s));
+      continue;
+    }
     std::atomic<int> failed{0};
     team.run([&](int t) {
       try {
@@ -633,8 +783,9 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
                                  dists, found, nexp, nadc, s));
     return;
   }
-  if (mode == GANN_MODE_STEPWISE_PAGED) {
-    run_stepwise_paged(h, q_dev, nq, topk, L, entries, nns, dists, found, nexp, nadc, s);
+  if (mode == GANN_MODE_STEPWISE_PAGED || mode == GANN_MODE_STEPWISE_URING) {
+    run_stepwise_paged(h, q_dev, nq, topk, L, entries, nns, dists, found, nexp, nadc, s,
+                       mode == GANN_MODE_STEPWISE_URING);
     return;
   }
   if (mode != GANN_MODE_STEPWISE) raise(GANN_ERR_INVALID, "unknown mode");

@@ -53,6 +53,10 @@ extern "C" {
                                       (src/hyd_task_runner.cu:200-275, src/io/mem_io.cpp:11-44);
                                       pages come from host memory (pinned placement) or the index
                                       file */
+#define GANN_MODE_STEPWISE_URING 5 /* GANN_MODE_STEPWISE_PAGED with every query's whole page read
+                                      from the index file through io_uring each round (O_DIRECT
+                                      where the file system allows; src/io/io_uring.cpp);
+                                      GANN_ERR_UNSUPPORTED where the kernel refuses io_uring */
 #define GANN_MODE_FUSED_GP 4  /* the shared-codebook fused kernel with the pivot table read from HBM
                                  through the caches and only the lists in LDS, forced (more lists
                                  per CU at large L) */

@@ -12,7 +12,8 @@ from _helpers import exact_pq, write_custom_index
 from test_search_semantics import random_graph
 
 import oracle as orc
-from gustann_amd import (FLOAT, MODE_FUSED, MODE_FUSED_GP, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED, UINT8,
+from gustann_amd import (FLOAT, MODE_FUSED, MODE_FUSED_GP, MODE_FUSED_LUT, MODE_STEPWISE, MODE_STEPWISE_PAGED,
+                         MODE_STEPWISE_URING, UINT8,
                          GannError, GustANN,
                          GustANNConfig, GustANNStats)
 from gustann_amd import index as gi
@@ -87,14 +88,16 @@ def test_stepwise_matches_fused_and_oracle(u8):
     _assert_same(got, (on, od, of), ne, oe)
 
 
-@pytest.mark.parametrize("pinned", [False, True])
-def test_paged_stepwise_matches_oracle(tiny_u8, pinned):
-    # pages come from the index file (HBM placement) or the pinned host image
+@pytest.mark.parametrize("pinned,mode", [(False, MODE_STEPWISE_PAGED), (True, MODE_STEPWISE_PAGED),
+                                         (False, MODE_STEPWISE_URING)])
+def test_paged_stepwise_matches_oracle(tiny_u8, pinned, mode):
+    # pages come from the index file (pread of the record, or whole pages
+    # through io_uring) or the pinned host image
     g = _open(_paths(tiny_u8), pinned=pinned)
     ix = orc.Index(*_paths(tiny_u8))
     Q = _queries(tiny_u8)[:120]
     ne = np.empty(Q.shape[0], np.int32)
-    got = g.search(Q, Q.shape[0], 10, 32, mode=MODE_STEPWISE_PAGED, n_exp=ne)
+    got = g.search(Q, Q.shape[0], 10, 32, mode=mode, n_exp=ne)
     on, od, of, oe, _ = ix.search(Q, 10, 32, threads=8)
     _assert_same(got, (on, od, of), ne, oe)
     g.close()
@@ -141,6 +144,8 @@ def test_fused_search_matches_oracle_float(tiny_f32, L):
     _assert_same(got4, (on, od, of))
     got5 = g.search(Q, Q.shape[0], 10, L, mode=MODE_FUSED_GP)
     _assert_same(got5, (on, od, of))
+    got6 = g.search(Q, Q.shape[0], 10, L, mode=MODE_STEPWISE_URING)
+    _assert_same(got6, (on, od, of))
     g.close()
 
 
@@ -158,7 +163,7 @@ def test_random_graphs_match_oracle(tmp_path, seed, R, L, topk, trained):
     ix = orc.Index(*paths[:2])
     Q = rng.integers(0, 256, (40, D)).astype(np.float32)
     on, od, of, oe, _ = ix.search(Q, topk, L)
-    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_FUSED_GP, MODE_STEPWISE, MODE_STEPWISE_PAGED):
+    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_FUSED_GP, MODE_STEPWISE, MODE_STEPWISE_PAGED, MODE_STEPWISE_URING):
         ne = np.empty(40, np.int32)
         got = g.search(Q, 40, topk, L, n_exp=ne, mode=mode)
         _assert_same(got, (on, od, of), ne, oe)
@@ -267,7 +272,7 @@ def test_zero_degree_nodes_match_oracle(tmp_path, seed):
     ix = orc.Index(*paths[:2])
     Q = rng.integers(0, 256, (30, D)).astype(np.float32)
     on, od, of, oe, _ = ix.search(Q, 5, 12)
-    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_FUSED_GP, MODE_STEPWISE, MODE_STEPWISE_PAGED):
+    for mode in (MODE_FUSED, MODE_FUSED_LUT, MODE_FUSED_GP, MODE_STEPWISE, MODE_STEPWISE_PAGED, MODE_STEPWISE_URING):
         ne = np.empty(30, np.int32)
         got = g.search(Q, 30, 5, 12, n_exp=ne, mode=mode)
         _assert_same(got, (on, od, of), ne, oe)
