@@ -19,6 +19,7 @@
 #include <chrono>
 #include <condition_variable>
 #include <functional>
+#include <memory>
 #include <mutex>
 #include <numeric>
 #include <random>
@@ -653,8 +654,10 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
   PageSource src;
   src.path = h->index_path;
   // io_uring: whole pages from the index file, O_DIRECT where the file
-  // system takes it (the reference's loader opens with O_DIRECT)
-  UringReader ring;
+  // system takes it (the reference's loader opens with O_DIRECT), one ring
+  // per host thread (the reference's one ring per context)
+  const int nthreads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+  std::vector<std::unique_ptr<UringReader>> rings;
   int ufd = -1;
   struct FdCloser {
     int& fd;
@@ -662,29 +665,30 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
       if (fd >= 0) ::close(fd);
     }
   } ufd_closer{ufd};
-  std::vector<std::pair<uint8_t*, off_t>> reqs;
+  std::vector<std::vector<std::pair<uint8_t*, off_t>>> reqs((size_t)nthreads);
   if (uring) {
     ufd = ::open(h->index_path.c_str(), O_RDONLY | O_DIRECT);
     if (ufd < 0) ufd = ::open(h->index_path.c_str(), O_RDONLY);
     if (ufd < 0) raise(GANN_ERR_IO, "cannot open " + h->index_path + " for page reads");
-    if (!ring.init(4096))
-      raise(GANN_ERR_UNSUPPORTED, std::string("io_uring is not available: ") + std::strerror(errno));
+    for (int t = 0; t < nthreads; ++t) {
+      rings.emplace_back(new UringReader());
+      if (!rings.back()->init(1024))
+        raise(GANN_ERR_UNSUPPORTED, std::string("io_uring is not available: ") + std::strerror(errno));
+    }
     // a file system that refuses O_DIRECT reads fails the first one: read
     // through the page cache then
-    reqs.assign(1, {(uint8_t*)h->slots.p, (off_t)0});
-    if (!ring.read_pages(ufd, reqs).empty()) {
+    reqs[0].assign(1, {(uint8_t*)h->slots.p, (off_t)0});
+    if (!rings[0]->read_pages(ufd, reqs[0]).empty()) {
       ::close(ufd);
       ufd = ::open(h->index_path.c_str(), O_RDONLY);
       if (ufd < 0) raise(GANN_ERR_IO, "cannot open " + h->index_path + " for page reads");
     }
-    reqs.reserve((size_t)nq);
   } else {
     src.open_for(h);
   }
   GANN_HIP(gann::launch_step_init(h->pq.dev, q_dev, nq, entries, h->luts.as<float>(), h->state.p, s));
   int32_t* active = h->counters.as<int32_t>() + 1;
   GANN_HIP(gann::launch_fill_i32(active, 1, nq, s));
-  const int nthreads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
   ThreadTeam team(nthreads);
   std::vector<int32_t> req((size_t)nq);
   const int64_t max_rounds = Ly.num_pts + 2;
@@ -702,13 +706,22 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
     if (n_active == 0) break;
     // submit_task: every active query's page (io_uring) or record into its slot
     if (uring) {
-      reqs.clear();
-      for (int32_t j = 0; j < nq; ++j)
-        if (req[(size_t)j] >= 0)
-          reqs.emplace_back((uint8_t*)h->slots.p + (size_t)j * gann::kSectorBytes,
-                            (off_t)((req[(size_t)j] / Ly.nodes_per_page + 1) * gann::kSectorBytes));
-      const std::string e = ring.read_pages(ufd, reqs);
-      if (!e.empty()) raise(GANN_ERR_IO, e + " (" + h->index_path + ")");
+      std::vector<std::string> errs((size_t)nthreads);
+      team.run([&](int t) {
+        try {
+          auto& rq = reqs[(size_t)t];
+          rq.clear();
+          for (int32_t j = t; j < nq; j += nthreads)
+            if (req[(size_t)j] >= 0)
+              rq.emplace_back((uint8_t*)h->slots.p + (size_t)j * gann::kSectorBytes,
+                              (off_t)((req[(size_t)j] / Ly.nodes_per_page + 1) * gann::kSectorBytes));
+          errs[(size_t)t] = rings[(size_t)t]->read_pages(ufd, rq);
+        } catch (...) {
+          errs[(size_t)t] = "page read request failed";
+        }
+      });
+      for (const std::string& e : errs)
+        if (!e.empty()) raise(GANN_ERR_IO, e + " (" + h->index_path + ")");
       GANN_HIP(gann::launch_step_round(h->ix, h->pq.dev, h->dtype, q_dev, nq, h->luts.as<float>(), topk,
                                        L, h->lists.as<uint64_t>(), h->state.p, nns, dists, active,
                                        (const uint8_t*)slots_dev, s));
