@@ -25,6 +25,7 @@
 #include <random>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <thread>
@@ -774,15 +775,37 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
     return;
   }
   if (mode == GANN_MODE_FUSED || mode == GANN_MODE_FUSED_GP) {
-    const bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
-    const int waves = gp ? w_gp : w_lds;
+    // Below kSplitWaves lists beside the whole table, keep all but its last
+    // group of 8 chunks in LDS (that group read through the caches) when
+    // that leaves room for kSplitWaves lists.
+    constexpr int kSplitWaves = 12;
+    const int chunk_w = h->pq.dev.chunk_w;
+    const int groups = gann::search_cb_split_groups(h->pq.dev.M, chunk_w);
+    bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
+    int g = 0;
+    if (mode == GANN_MODE_FUSED && w_lds < kSplitWaves && groups > 1 &&
+        gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true, groups - 1, chunk_w) >= kSplitWaves) {
+      g = groups - 1;
+      gp = true;
+    }
+    // tuning override: "split" or "cache" forces that form
+    if (const char* e = std::getenv("GANN_PIVOT_FORM")) {
+      if (!std::strcmp(e, "split") && groups > 1) {
+        g = groups - 1;
+        gp = true;
+      } else if (!std::strcmp(e, "cache")) {
+        g = 0;
+        gp = true;
+      }
+    }
+    const int waves = gp ? gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true, g, chunk_w) : w_lds;
     if (waves >= 1 && (gp || waves >= 2)) {
       h->counters.ensure(64);
       h->qs.ensure((size_t)nq * Ly.dim * 4);
       const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
       GANN_HIP(gann::launch_search_cb(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,
                                       dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
-                                      h->qs.as<float>(), waves, blocks, gp, s));
+                                      h->qs.as<float>(), waves, blocks, gp, gp ? g : 0, s));
       return;
     }
     if (mode == GANN_MODE_FUSED_GP)

@@ -381,6 +381,11 @@ struct CbSmem {
   static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * dim * 4 + 240; }
 };
 
+// LDS bytes of the first g groups of 8 chunks of W dims, in the cb_row layout.
+__host__ __device__ constexpr size_t split_pivot_bytes(int g, int W) {
+  return g > 0 ? (size_t)kPivots * g * 8 * W * 4 + 240 : 0;
+}
+
 __device__ __forceinline__ uint32_t cb_row(uint32_t c, uint32_t rowb) {
   return __umul24(c, rowb) + (c & 0xF0u);
 }
@@ -422,10 +427,12 @@ struct PivotVec<2> {
 // q - mu is read 8 chunks at a time with uniform loads from qs, whose
 // address is made opaque per group so the compiler does not keep all of it
 // in scalar registers across expansions.
-template <int W, int MW>
+// kSplitG > 0: groups of 8 chunks below kSplitG come from the partial
+// table pivl in LDS (rows of kSplitG * 8 * W floats), the others from piv.
+template <int W, int MW, int kSplitG = 0>
 __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uint32_t rowb,
                                         const PQDev& pq, const CodeRow<MW>& row,
-                                        const uint8_t* crow) {
+                                        const uint8_t* crow, const uint8_t* pivl = nullptr) {
   float dist = 0.0f;
   if constexpr (MW > 0 && (W == 4 || W == 2)) {
     typedef typename PivotVec<W>::type PV;
@@ -435,11 +442,14 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         PV p[8];
+        const bool from_lds = 2 * k + h < kSplitG;  // compile-time
+        const uint8_t* base = from_lds ? pivl : piv;
+        const uint32_t stride = from_lds ? (uint32_t)(kSplitG * 8 * W * 4) : rowb;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
           const int bb = 8 * h + b;
           const uint32_t c = (ws[bb >> 2] >> (8 * (bb & 3))) & 0xffu;
-          p[b] = *reinterpret_cast<const PV*>(piv + cb_row(c, rowb) + (16 * k + bb) * W * 4);
+          p[b] = *reinterpret_cast<const PV*>(base + cb_row(c, stride) + (16 * k + bb) * W * 4);
         }
         // uniform address in the constant address space: scalar loads
         uint64_t qa = (uint64_t)(qs + (16 * k + 8 * h) * W);
@@ -476,7 +486,7 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
 // kGP: the pivot table is read from pq.piv_cb (HBM, through the caches)
 // instead of a copy in LDS, which then holds only the per-wave lists: the
 // form for large L, where lists beside a 128 KB table leave few waves.
-template <typename T, int MW, int W, bool kGP>
+template <typename T, int MW, int W, bool kGP, int kSplitG = 0>
 __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
                                                          const float* __restrict__ q, int nq,
                                                          const int32_t* __restrict__ entries,
@@ -494,6 +504,16 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
   size_t lists_at = 0;
   if constexpr (kGP) {
     piv = (const uint8_t*)((const __attribute__((address_space(1))) uint8_t*)pq.piv_cb);
+    if constexpr (kSplitG > 0) {
+      // the first kSplitG groups of 8 chunks also in LDS
+      constexpr int per_row = kSplitG * 8 * W;
+      for (int idx = threadIdx.x; idx < kPivots * per_row; idx += blockDim.x) {
+        const int c = idx / per_row, i = idx - c * per_row;
+        *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, per_row * 4) + 4 * i) = pq.pivots[c * dim + i];
+      }
+      __syncthreads();
+      lists_at = split_pivot_bytes(kSplitG, W);
+    }
   } else {
     piv = smem_raw;
     lists_at = CbSmem::pivot_bytes(dim);
@@ -537,7 +557,7 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
         CodeRow<MW> row;
         const uint8_t* crow = pq.codes + (int64_t)cur.v * M;
         row.load(crow, M);
-        key = make_key(cb_adc<W, MW>(piv, qs, rowb, pq, row, crow), cur.v);
+        key = make_key(cb_adc<W, MW, kSplitG>(piv, qs, rowb, pq, row, crow, smem_raw), cur.v);
       }
       const float du = cur.l2(qv, dim);
       const ListPlan P = list_plan(A, L, key, deg, sz, fu);
@@ -982,10 +1002,16 @@ hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const f
                                 stream);
 }
 
-int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots) {
-  const size_t piv = global_pivots ? 0 : CbSmem::pivot_bytes(dim), w = CbSmem::wave_bytes(dim, L, topk);
+int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots, int lds_groups,
+                    int chunk_w) {
+  const size_t piv = global_pivots ? split_pivot_bytes(lds_groups, chunk_w) : CbSmem::pivot_bytes(dim);
+  const size_t w = CbSmem::wave_bytes(dim, L, topk);
   if (piv + w > lds_limit) return 0;
   return (int)std::min<size_t>(16, (lds_limit - piv) / w);
+}
+
+int search_cb_split_groups(int M, int chunk_w) {
+  return (mw_of(M) > 0 && (chunk_w == 2 || chunk_w == 4)) ? M / 8 : 0;
 }
 
 size_t search_cb_pivot_bytes(int dim) { return CbSmem::pivot_bytes(dim); }
@@ -1001,9 +1027,12 @@ void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out) {
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                            float* qs_all, int waves, int blocks, bool global_pivots, hipStream_t stream) {
+                            float* qs_all, int waves, int blocks, bool global_pivots, int lds_groups,
+                            hipStream_t stream) {
   if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
-  const size_t smem = (global_pivots ? 0 : CbSmem::pivot_bytes(ix.dim)) +
+  const int split = search_cb_split_groups(pq.M, pq.chunk_w);
+  if (lds_groups != 0 && (!global_pivots || lds_groups != split - 1)) return hipErrorInvalidValue;
+  const size_t smem = (global_pivots ? split_pivot_bytes(lds_groups, pq.chunk_w) : CbSmem::pivot_bytes(ix.dim)) +
                       (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
   hipError_t e = launch_fill_i32(queue, 1, 0, stream);
   if (e != hipSuccess) return e;
@@ -1016,14 +1045,20 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
     using T = decltype(t);
     return with_mw(pq.M, [&](auto mw) {
       return with_w(pq.chunk_w, [&](auto w) {
-        if (global_pivots)
-          hipLaunchKernelGGL((search_cb_kernel<T, decltype(mw)::value, decltype(w)::value, true>),
-                             dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries,
-                             topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+        constexpr int MWv = decltype(mw)::value, Wv = decltype(w)::value;
+        constexpr int kSplit = (MWv > 0 && (Wv == 2 || Wv == 4)) ? 2 * MWv - 1 : 0;
+        if (global_pivots && lds_groups > 0 && kSplit > 0)
+          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kSplit>), dim3(blocks), dim3(waves * kWave),
+                             smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
+                             queue, qs_all);
+        else if (global_pivots)
+          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true>), dim3(blocks), dim3(waves * kWave), smem,
+                             stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
+                             qs_all);
         else
-          hipLaunchKernelGGL((search_cb_kernel<T, decltype(mw)::value, decltype(w)::value, false>),
-                             dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries,
-                             topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, false>), dim3(blocks), dim3(waves * kWave), smem,
+                             stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
+                             qs_all);
         return hipGetLastError();
       });
     });

@@ -30,8 +30,13 @@ hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const f
                          const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                          int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
 // Shared-codebook search: waves per workgroup that fit the LDS (0 = does not
-// fit), with the pivot table in LDS or (global_pivots) read from pq.piv_cb.
-int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots = false);
+// fit), with the pivot table in LDS or (global_pivots) read from pq.piv_cb,
+// the first lds_groups groups of 8 chunks (chunk_w dims each) still in LDS.
+int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots = false,
+                    int lds_groups = 0, int chunk_w = 0);
+// Groups of 8 chunks of the pivot table (0: the split form is not
+// available); the split form keeps all but the last group in LDS.
+int search_cb_split_groups(int M, int chunk_w);
 // Size and contents of pq.piv_cb: the pivots [256][dim] in the kernel's row layout.
 size_t search_cb_pivot_bytes(int dim);
 void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out);
@@ -39,7 +44,7 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
                             float* qs_all, int waves, int blocks, bool global_pivots,
-                            hipStream_t stream);
+                            int lds_groups, hipStream_t stream);
 // Beam search with beam width bw in [2, max_beam_width()] (same LDS layout,
 // pivot placement and launch shape as launch_search_cb).
 hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,

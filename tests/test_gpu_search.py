@@ -281,3 +281,18 @@ def test_zero_degree_nodes_match_oracle(tmp_path, seed):
     got = g.search(Q, 30, 5, 12, beam_width=3, n_exp=ne)
     _assert_same(got, (bn, bd, bf), ne, be)
     g.close()
+
+
+@pytest.mark.parametrize("form", ["split", "cache"])
+def test_pivot_table_forms_match_oracle(u8, form, monkeypatch):
+    # all but the last group of 8 chunks of the pivot table in LDS ("split"),
+    # or the whole table read through the caches ("cache"); GANN_PIVOT_FORM
+    # forces the form at every L
+    meta, g, ix = u8
+    Q = _queries(meta)
+    monkeypatch.setenv("GANN_PIVOT_FORM", form)
+    for L, topk in ((40, 10), (300, 10), (200, 100)):
+        ne = np.empty(Q.shape[0], np.int32)
+        got = g.search(Q, Q.shape[0], topk, L, n_exp=ne)
+        on, od, of, oe, _ = ix.search(Q, topk, L, threads=8)
+        _assert_same(got, (on, od, of), ne, oe)
