@@ -776,22 +776,31 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
   }
   if (mode == GANN_MODE_FUSED || mode == GANN_MODE_FUSED_GP) {
     // Below kSplitWaves lists beside the whole table, keep all but its last
-    // group of 8 chunks in LDS (that group read through the caches) when
-    // that leaves room for kSplitWaves lists.
-    constexpr int kSplitWaves = 12;
+    // group of 8 chunks in LDS, or else its first half, when that leaves room
+    // for kSplitWaves lists (measured on the 10M uint8 index: the half table
+    // with 11 lists beats the cache-read table with 16 at L=1024); the groups
+    // not in LDS are read through the caches.
+    constexpr int kSplitWaves = 11;
     const int chunk_w = h->pq.dev.chunk_w;
     const int groups = gann::search_cb_split_groups(h->pq.dev.M, chunk_w);
     bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
     int g = 0;
-    if (mode == GANN_MODE_FUSED && w_lds < kSplitWaves && groups > 1 &&
-        gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true, groups - 1, chunk_w) >= kSplitWaves) {
-      g = groups - 1;
-      gp = true;
+    if (mode == GANN_MODE_FUSED && w_lds < kSplitWaves && groups > 1) {
+      for (int c : {groups - 1, groups / 2})
+        if (gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true, c, chunk_w) >= kSplitWaves) {
+          g = c;
+          gp = true;
+          break;
+        }
     }
-    // tuning override: "split" or "cache" forces that form
+    // tuning override: "split" (all groups but one in LDS), "half" or
+    // "cache" (none in LDS) forces that form
     if (const char* e = std::getenv("GANN_PIVOT_FORM")) {
       if (!std::strcmp(e, "split") && groups > 1) {
         g = groups - 1;
+        gp = true;
+      } else if (!std::strcmp(e, "half") && groups > 1) {
+        g = groups / 2;
         gp = true;
       } else if (!std::strcmp(e, "cache")) {
         g = 0;

@@ -1031,7 +1031,8 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
                             hipStream_t stream) {
   if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
   const int split = search_cb_split_groups(pq.M, pq.chunk_w);
-  if (lds_groups != 0 && (!global_pivots || lds_groups != split - 1)) return hipErrorInvalidValue;
+  if (lds_groups != 0 && (!global_pivots || (lds_groups != split - 1 && lds_groups != split / 2)))
+    return hipErrorInvalidValue;
   const size_t smem = (global_pivots ? split_pivot_bytes(lds_groups, pq.chunk_w) : CbSmem::pivot_bytes(ix.dim)) +
                       (size_t)waves * CbSmem::wave_bytes(ix.dim, L, topk);
   hipError_t e = launch_fill_i32(queue, 1, 0, stream);
@@ -1046,9 +1047,14 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
     return with_mw(pq.M, [&](auto mw) {
       return with_w(pq.chunk_w, [&](auto w) {
         constexpr int MWv = decltype(mw)::value, Wv = decltype(w)::value;
-        constexpr int kSplit = (MWv > 0 && (Wv == 2 || Wv == 4)) ? 2 * MWv - 1 : 0;
-        if (global_pivots && lds_groups > 0 && kSplit > 0)
+        constexpr bool kCanSplit = MWv > 0 && (Wv == 2 || Wv == 4);
+        constexpr int kSplit = kCanSplit ? 2 * MWv - 1 : 0, kHalf = kCanSplit ? MWv : 0;
+        if (global_pivots && lds_groups > 0 && kCanSplit && lds_groups == kSplit)
           hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kSplit>), dim3(blocks), dim3(waves * kWave),
+                             smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
+                             queue, qs_all);
+        else if (global_pivots && lds_groups > 0 && kCanSplit && lds_groups == kHalf)
+          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kHalf>), dim3(blocks), dim3(waves * kWave),
                              smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
                              queue, qs_all);
         else if (global_pivots)

@@ -34,8 +34,9 @@ hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const f
 // the first lds_groups groups of 8 chunks (chunk_w dims each) still in LDS.
 int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots = false,
                     int lds_groups = 0, int chunk_w = 0);
-// Groups of 8 chunks of the pivot table (0: the split form is not
-// available); the split form keeps all but the last group in LDS.
+// Groups of 8 chunks of the pivot table (0: the split forms are not
+// available); the split forms keep all but the last group, or the first
+// half of the groups, in LDS (lds_groups = groups - 1 or groups / 2).
 int search_cb_split_groups(int M, int chunk_w);
 // Size and contents of pq.piv_cb: the pivots [256][dim] in the kernel's row layout.
 size_t search_cb_pivot_bytes(int dim);

@@ -283,11 +283,11 @@ def test_zero_degree_nodes_match_oracle(tmp_path, seed):
     g.close()
 
 
-@pytest.mark.parametrize("form", ["split", "cache"])
+@pytest.mark.parametrize("form", ["split", "half", "cache"])
 def test_pivot_table_forms_match_oracle(u8, form, monkeypatch):
     # all but the last group of 8 chunks of the pivot table in LDS ("split"),
-    # or the whole table read through the caches ("cache"); GANN_PIVOT_FORM
-    # forces the form at every L
+    # its first half ("half"), or the whole table read through the caches
+    # ("cache"); GANN_PIVOT_FORM forces the form at every L
     meta, g, ix = u8
     Q = _queries(meta)
     monkeypatch.setenv("GANN_PIVOT_FORM", form)
