@@ -1333,7 +1333,8 @@ int gann_build_vamana(const uint8_t* data, int64_t n, int32_t dim, int32_t R, in
     };
     DevBuf x, xn, nbr, deg, ord, sums, mean, best;
     upload_build_rows(data, n, dim, dp, x, xn);
-    nbr.ensure((size_t)n * R * 4);
+    const int C = gann::build_capacity(R);  // lists grow to C before a prune (graph slack)
+    nbr.ensure((size_t)n * C * 4);
     deg.ensure((size_t)n * 4);
     // medoid: the point closest to the mean
     sums.ensure((size_t)dp * 8);
@@ -1355,7 +1356,7 @@ int gann_build_vamana(const uint8_t* data, int64_t n, int32_t dim, int32_t R, in
     if ((int64_t)medoid >= n) raise(GANN_ERR_FORMAT, "graph build: medoid search failed");
     // random initial graph and the insertion order
     const int init_deg = (int)std::min<int64_t>(R / 2 > 0 ? R / 2 : 1, n - 1);
-    gann::BuildDev g{x.as<uint8_t>(), xn.as<int32_t>(), nbr.as<uint32_t>(), deg.as<uint32_t>(), n, dp, R};
+    gann::BuildDev g{x.as<uint8_t>(), xn.as<int32_t>(), nbr.as<uint32_t>(), deg.as<uint32_t>(), n, dp, R, C};
     GANN_HIP(gann::launch_build_random_graph(g, init_deg, seed, 0));
     {
       std::vector<uint32_t> order((size_t)n);
@@ -1410,7 +1411,20 @@ int gann_build_vamana(const uint8_t* data, int64_t n, int32_t dim, int32_t R, in
         }
       }
     }
-    GANN_HIP(hipMemcpy(out_nbr, nbr.p, (size_t)n * R * 4, hipMemcpyDeviceToHost));
+    // every list back to at most R
+    GANN_HIP(hipMemsetAsync(queue.p, 0, 4, 0));
+    GANN_HIP(gann::launch_build_final_prune(g, alpha, queue.as<int32_t>(), cus, (size_t)lds, 0));
+    GANN_HIP(hipDeviceSynchronize());
+    if (verbose) std::fprintf(stderr, "[gpu-vamana] final prune done (%.1f s)\n", secs());
+    pool_id.release();
+    pool_d.release();
+    pa.release();
+    pb.release();
+    temp.release();
+    DevBuf packed;
+    packed.ensure((size_t)n * R * 4);
+    GANN_HIP(gann::launch_build_compact(g, packed.as<uint32_t>(), 0));
+    GANN_HIP(hipMemcpy(out_nbr, packed.p, (size_t)n * R * 4, hipMemcpyDeviceToHost));
     GANN_HIP(hipMemcpy(out_deg, deg.p, (size_t)n * 4, hipMemcpyDeviceToHost));
     *out_medoid = (int64_t)medoid;
   });
@@ -1461,7 +1475,7 @@ int gann_diag_robust_prune(const uint8_t* data, int64_t n, int32_t dim, int64_t 
     const int dp = gann::build_row_bytes(dim);
     if (dp == 0) raise(GANN_ERR_UNSUPPORTED, "dim must be in [1, 256]");
     if (R < 1 || R > 64) raise(GANN_ERR_UNSUPPORTED, "R must be in [1, 64]");
-    if (ncand < 0 || ncand > gann::kBuildCandMax) raise(GANN_ERR_UNSUPPORTED, "ncand must be in [0, 192]");
+    if (ncand < 0 || ncand > gann::kBuildCandMax) raise(GANN_ERR_UNSUPPORTED, "ncand must be in [0, " + std::to_string(gann::kBuildCandMax) + "]");
     if (std::isnan(alpha)) raise(GANN_ERR_INVALID, "alpha is NaN");
     for (int32_t i = 0; i < ncand; ++i)
       if ((int64_t)cand[i] >= n) raise(GANN_ERR_INVALID, "candidate id outside [0, n)");
@@ -1475,7 +1489,7 @@ int gann_diag_robust_prune(const uint8_t* data, int64_t n, int32_t dim, int64_t 
     dout.ensure((size_t)R * 4);
     dn.ensure(4);
     if (ncand > 0) GANN_HIP(hipMemcpy(dc.p, cand, (size_t)ncand * 4, hipMemcpyHostToDevice));
-    gann::BuildDev g{x.as<uint8_t>(), xn.as<int32_t>(), nbr.as<uint32_t>(), deg.as<uint32_t>(), n, dp, R};
+    gann::BuildDev g{x.as<uint8_t>(), xn.as<int32_t>(), nbr.as<uint32_t>(), deg.as<uint32_t>(), n, dp, R, R};
     GANN_HIP(gann::launch_build_prune_one(g, (uint32_t)p, dc.as<uint32_t>(), ncand, alpha, dout.as<uint32_t>(),
                                           dn.as<int32_t>(), (size_t)lds, 0));
     int32_t k = 0;

@@ -16,8 +16,11 @@
 //      requests (target << 32 | source).
 //   3. the requests are sorted by target and each target's run is handled by
 //      one wavefront (build_reverse_kernel): appended while the list has
-//      room, else the list and the new sources are pruned back to R.
-// Points of one batch see the graph as it was when the batch started.
+//      room (up to C = ceil(1.3 R), DiskANN's slack), else the list and the
+//      new sources are pruned back to R.
+//   4. after the passes, lists longer than R are pruned back to R.
+// Points of one batch see the graph as it was when the batch started; the
+// searches follow the first R entries of each list.
 // Distances are exact: |a|^2 + |b|^2 - 2 a.b with v_dot4_u32_u8, below 2^24
 // for dim <= 256, so they are exact floats equal to the host builder's.
 #include "gann_build.hpp"
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(256) void random_graph_kernel(BuildDev g, int init_
   const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (u >= g.n) return;
   DevRng r(seed, (uint64_t)u + 1);
-  uint32_t* out = g.nbr + u * g.R;
+  uint32_t* out = g.nbr + u * g.C;
   int k = 0;
   for (int draws = 0; k < init_deg && draws < kMaxDraws; ++draws) {
     const uint32_t v = (uint32_t)r.below((uint64_t)g.n);
@@ -221,7 +224,6 @@ __global__ __launch_bounds__(256) void build_search_kernel(BuildDev g, const uin
   uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + kBuildPoolMax);
-  const int R = g.R;
   const int64_t cap = g.n + 2;
   for (;;) {
     int qi = 0;
@@ -237,14 +239,34 @@ __global__ __launch_bounds__(256) void build_search_kernel(BuildDev g, const uin
     int sz = 0, fu = 0;
     TopK top(td, ti, kBuildPoolMax);
     for (int64_t exps = 1;; ++exps) {
-      const int deg = __builtin_amdgcn_readfirstlane((int)min(g.deg[u], (uint32_t)R));
+      // up to C neighbours (a list in its slack), 64 per list update
+      const int deg = __builtin_amdgcn_readfirstlane((int)min(g.deg[u], (uint32_t)g.C));
+      int part = 0;
+      for (; part + kWave < deg; part += kWave) {
+        uint64_t key = ~(uint64_t)0;
+        const uint32_t v = g.nbr[(int64_t)u * g.C + part + lane];
+        if ((int64_t)v < g.n)
+          key = make_key(sq_dist(np, g.xn[v], row_dot<NC>(w, g.x + (int64_t)v * g.dp)), v);
+        const ListPlan Pi = list_plan(A, L, key, kWave, sz, fu);
+        int lb = list_apply<false>(A, BM, Pi);
+        sz = Pi.nsz;
+        // the exact first unvisited entry for the next update
+        for (fu = sz; lb < sz; lb += kWave) {
+          const uint64_t m = ballot64(lb + lane < sz && !entry_visited(A[lb + lane]));
+          if (m) {
+            fu = lb + (int)__builtin_ctzll(m);
+            break;
+          }
+        }
+      }
+      const int dl = deg - part;
       uint64_t key = ~(uint64_t)0;  // padding and out-of-range ids sort last and are dropped
-      if (lane < deg) {
-        const uint32_t v = g.nbr[(int64_t)u * R + lane];
+      if (lane < dl) {
+        const uint32_t v = g.nbr[(int64_t)u * g.C + part + lane];
         if ((int64_t)v < g.n)
           key = make_key(sq_dist(np, g.xn[v], row_dot<NC>(w, g.x + (int64_t)v * g.dp)), v);
       }
-      const ListPlan P = list_plan(A, L, key, deg, sz, fu);
+      const ListPlan P = list_plan(A, L, key, dl, sz, fu);
       fu = list_apply(A, BM, P);
       sz = P.nsz;
       top.push(du, (int32_t)u);
@@ -261,12 +283,14 @@ __global__ __launch_bounds__(256) void build_search_kernel(BuildDev g, const uin
 // ------------------------------------------------------------------ RobustPrune
 
 // Per-wave LDS: keys | sorted keys | occlusion | norms | ids (kBuildCandMax
-// each) | kept list (64) | candidate rows (stride dp + 16: the 16-byte
-// reads of 16 consecutive lanes fall on distinct banks).
+// each) | kept or current list (kOutWords) | candidate rows (stride dp + 16:
+// the 16-byte reads of 16 consecutive lanes fall on distinct banks).
+constexpr int kOutWords = 128;
+static_assert(kOutWords >= kBuildSlackMax && kOutWords >= kWave, "list buffer");
 struct PruneSmem {
   static __host__ __device__ size_t row_stride(int dp) { return (size_t)dp + 16; }
   static __host__ __device__ size_t bytes(int dp) {
-    const size_t b = (size_t)kBuildCandMax * (8 + 8 + 4 + 4 + 4) + 64 * 4 +
+    const size_t b = (size_t)kBuildCandMax * (8 + 8 + 4 + 4 + 4) + kOutWords * 4 +
                      row_stride(dp) * kBuildCandMax;
     return (b + 15) & ~(size_t)15;
   }
@@ -284,7 +308,7 @@ struct PruneSmem {
     cn = reinterpret_cast<int32_t*>(occl + kBuildCandMax);
     cid = reinterpret_cast<uint32_t*>(cn + kBuildCandMax);
     outl = cid + kBuildCandMax;
-    rows = reinterpret_cast<uint8_t*>(outl + 64);
+    rows = reinterpret_cast<uint8_t*>(outl + kOutWords);
   }
 };
 
@@ -374,7 +398,7 @@ __device__ int prune_wave(const BuildDev& g, uint32_t p, int nc, float alpha, co
     wave_sync();
   }
   wave_sync();
-  if (lane < kept) g.nbr[(int64_t)p * g.R + lane] = S.outl[lane];
+  if (lane < kept) g.nbr[(int64_t)p * g.C + lane] = S.outl[lane];
   if (lane == 0) g.deg[p] = (uint32_t)kept;
   return kept;
 }
@@ -396,17 +420,20 @@ __global__ __launch_bounds__(256) void build_prune_fwd_kernel(BuildDev g, const 
     qi = __builtin_amdgcn_readfirstlane(__shfl(qi, 0, kWave));
     if (qi >= npts) break;
     const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane((int)pts[qi]);
-    const int npool = __builtin_amdgcn_readfirstlane(min(max(pool_n[qi], 0), kBuildPoolMax));
+    const int dg = __builtin_amdgcn_readfirstlane((int)min(g.deg[p], (uint32_t)g.C));
+    // the pool (sorted by distance) keeps its closest entries when it and
+    // the current list exceed the candidate buffer
+    const int npool =
+        __builtin_amdgcn_readfirstlane(min(min(max(pool_n[qi], 0), kBuildPoolMax), kBuildCandMax - dg));
     for (int j = lane; j < npool; j += kWave)
       S.keys[j] = make_key(pool_d[(int64_t)qi * kBuildPoolMax + j], pool_id[(int64_t)qi * kBuildPoolMax + j]);
-    const int dg = __builtin_amdgcn_readfirstlane((int)min(g.deg[p], (uint32_t)R));
     if (dg > 0) {
       uint32_t w[4 * NC];
       uniform_row<NC>(g.x, g.dp, p, w);
       const int32_t np = __builtin_amdgcn_readfirstlane(g.xn[p]);
-      if (lane < dg) {
-        const uint32_t v = g.nbr[(int64_t)p * R + lane];
-        S.keys[npool + lane] = make_key(sq_dist(np, g.xn[v], row_dot<NC>(w, g.x + (int64_t)v * g.dp)), v);
+      for (int j = lane; j < dg; j += kWave) {
+        const uint32_t v = g.nbr[(int64_t)p * g.C + j];
+        S.keys[npool + j] = make_key(sq_dist(np, g.xn[v], row_dot<NC>(w, g.x + (int64_t)v * g.dp)), v);
       }
     }
     const int kept = prune_wave<NC>(g, p, npool + dg, alpha, S);
@@ -433,7 +460,6 @@ __global__ __launch_bounds__(256) void build_reverse_kernel(BuildDev g, const un
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int lane = lane_id();
   const PruneSmem S(smem_raw + (size_t)(threadIdx.x >> 6) * PruneSmem::bytes(g.dp));
-  const int R = g.R;
   const int ns = __builtin_amdgcn_readfirstlane(*n_seg);
   for (;;) {
     int s = 0;
@@ -444,8 +470,8 @@ __global__ __launch_bounds__(256) void build_reverse_kernel(BuildDev g, const un
     const int64_t b = s + 1 < ns ? (int64_t)seg_start[s + 1] : npairs;
     const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(pairs[a] >> 32));
     if ((int64_t)v >= g.n) continue;  // the run of unused slots
-    const int dv = __builtin_amdgcn_readfirstlane((int)min(g.deg[v], (uint32_t)R));
-    if (lane < dv) S.outl[lane] = g.nbr[(int64_t)v * R + lane];
+    const int dv = __builtin_amdgcn_readfirstlane((int)min(g.deg[v], (uint32_t)g.C));
+    for (int e = lane; e < dv; e += kWave) S.outl[e] = g.nbr[(int64_t)v * g.C + e];
     wave_sync();
     // new sources: not listed yet, at most kBuildCandMax - dv of them
     const int room = kBuildCandMax - dv;
@@ -461,8 +487,8 @@ __global__ __launch_bounds__(256) void build_reverse_kernel(BuildDev g, const un
       m_new = min(m_new + (int)__popcll(mask), room);
     }
     wave_sync();
-    if (dv + m_new <= R) {
-      if (lane < m_new) g.nbr[(int64_t)v * R + dv + lane] = S.cid[lane];
+    if (dv + m_new <= g.C) {
+      for (int e = lane; e < m_new; e += kWave) g.nbr[(int64_t)v * g.C + dv + e] = S.cid[e];
       if (lane == 0) g.deg[v] = (uint32_t)(dv + m_new);
     } else {
       uint32_t w[4 * NC];
@@ -476,6 +502,47 @@ __global__ __launch_bounds__(256) void build_reverse_kernel(BuildDev g, const un
     }
     wave_sync();
   }
+}
+
+// Lists longer than R pruned back to R, one wavefront per node.
+template <int NC>
+__global__ __launch_bounds__(256) void build_final_prune_kernel(BuildDev g, float alpha, int32_t* __restrict__ queue) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  const int lane = lane_id();
+  const PruneSmem S(smem_raw + (size_t)(threadIdx.x >> 6) * PruneSmem::bytes(g.dp));
+  for (;;) {
+    int base = 0;
+    if (lane == 0) base = atomicAdd(queue, kWave);
+    base = __builtin_amdgcn_readfirstlane(__shfl(base, 0, kWave));
+    if ((int64_t)base >= g.n) break;
+    // the lanes' nodes, then the long lists among them one at a time
+    const int64_t mine = (int64_t)base + lane;
+    const bool longer = mine < g.n && (int)g.deg[mine] > g.R;
+    uint64_t todo = ballot64(longer);
+    while (todo) {
+      const int l = (int)__builtin_ctzll(todo);
+      todo &= todo - 1;
+      const uint32_t v = (uint32_t)(base + l);
+      const int dv = __builtin_amdgcn_readfirstlane((int)min(g.deg[v], (uint32_t)g.C));
+      uint32_t w[4 * NC];
+      uniform_row<NC>(g.x, g.dp, v, w);
+      const int32_t nv = __builtin_amdgcn_readfirstlane(g.xn[v]);
+      for (int c = lane; c < dv; c += kWave) {
+        const uint32_t id = g.nbr[(int64_t)v * g.C + c];
+        S.keys[c] = make_key(sq_dist(nv, g.xn[id], row_dot<NC>(w, g.x + (int64_t)id * g.dp)), id);
+      }
+      prune_wave<NC>(g, v, dv, alpha, S);
+      wave_sync();
+    }
+  }
+}
+
+// The lists in rows of R entries (out [n][R]) for one contiguous download.
+__global__ __launch_bounds__(256) void compact_rows_kernel(const uint32_t* __restrict__ nbr, int64_t n, int C, int R,
+                                                           uint32_t* __restrict__ out) {
+  const int64_t total = n * R;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = nbr[(i / R) * C + i % R];
 }
 
 // One RobustPrune of p over explicit candidates (diagnostic entry).
@@ -589,7 +656,7 @@ hipError_t launch_build_medoid(const uint8_t* x, int64_t n, int dim, int dp, con
 }
 
 hipError_t launch_build_random_graph(BuildDev g, int init_deg, uint64_t seed, hipStream_t stream) {
-  if (init_deg > g.R) return hipErrorInvalidValue;
+  if (init_deg > g.R || g.C < g.R) return hipErrorInvalidValue;
   hipLaunchKernelGGL(random_graph_kernel, dim3(grid_for(g.n, 256)), dim3(256), 0, stream, g, init_deg, seed);
   return hipGetLastError();
 }
@@ -599,7 +666,7 @@ size_t build_search_smem_bytes(int L, int waves) { return search_wave_bytes(L) *
 hipError_t launch_build_search(BuildDev g, const uint32_t* pts, int npts, uint32_t start, int L,
                                uint32_t* pool_id, float* pool_d, int32_t* pool_n, int32_t* queue, int cus,
                                hipStream_t stream) {
-  if (g.R < 1 || g.R > kWave || L < 1) return hipErrorInvalidValue;
+  if (g.R < 1 || g.R > kWave || g.C < g.R || g.C > kBuildSlackMax || L < 1) return hipErrorInvalidValue;
   const size_t smem = build_search_smem_bytes(L, 4);
   const unsigned grid = (unsigned)std::max(1, std::min(8 * cus, (npts + 3) / 4));
   return with_nc(g.dp, [&](auto nc) {
@@ -618,7 +685,7 @@ hipError_t launch_build_prune_fwd(BuildDev g, const uint32_t* pts, int npts, con
                                   const float* pool_d, const int32_t* pool_n, float alpha,
                                   unsigned long long* pairs, int32_t* queue, int cus, size_t lds_limit,
                                   hipStream_t stream) {
-  if (g.R < 1 || g.R > kWave) return hipErrorInvalidValue;
+  if (g.R < 1 || g.R > kWave || g.C < g.R || g.C > kBuildSlackMax) return hipErrorInvalidValue;
   const int waves = build_prune_waves(g.dp, lds_limit);
   if (waves < 1) return hipErrorInvalidValue;
   const size_t smem = PruneSmem::bytes(g.dp) * (size_t)waves;
@@ -659,7 +726,7 @@ hipError_t launch_build_segments(void* temp, size_t temp_bytes, const unsigned l
 hipError_t launch_build_reverse(BuildDev g, const unsigned long long* pairs, int64_t npairs,
                                 const int32_t* seg_start, const int32_t* n_seg, float alpha, int32_t* queue,
                                 int cus, size_t lds_limit, hipStream_t stream) {
-  if (g.R < 1 || g.R > kWave) return hipErrorInvalidValue;
+  if (g.R < 1 || g.R > kWave || g.C < g.R || g.C > kBuildSlackMax) return hipErrorInvalidValue;
   const int waves = build_prune_waves(g.dp, lds_limit);
   if (waves < 1) return hipErrorInvalidValue;
   const size_t smem = PruneSmem::bytes(g.dp) * (size_t)waves;
@@ -685,9 +752,29 @@ hipError_t launch_pq_encode(const void* x, int dtype, int64_t n, int dim, const 
   return hipGetLastError();
 }
 
+hipError_t launch_build_final_prune(BuildDev g, float alpha, int32_t* queue, int cus, size_t lds_limit,
+                                    hipStream_t stream) {
+  if (g.R < 1 || g.R > kWave || g.C < g.R || g.C > kBuildSlackMax) return hipErrorInvalidValue;
+  const int waves = build_prune_waves(g.dp, lds_limit);
+  if (waves < 1) return hipErrorInvalidValue;
+  const size_t smem = PruneSmem::bytes(g.dp) * (size_t)waves;
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2 * cus, (g.n + 63) / 64));
+  return with_nc(g.dp, [&](auto nc) {
+    hipLaunchKernelGGL(build_final_prune_kernel<decltype(nc)::value>, dim3(grid), dim3(64 * waves), smem, stream,
+                       g, alpha, queue);
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_build_compact(BuildDev g, uint32_t* out, hipStream_t stream) {
+  const unsigned grid = (unsigned)std::min<int64_t>(16384, grid_for(g.n * g.R, 256));
+  hipLaunchKernelGGL(compact_rows_kernel, dim3(grid), dim3(256), 0, stream, g.nbr, g.n, g.C, g.R, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_build_prune_one(BuildDev g, uint32_t p, const uint32_t* cand, int ncand, float alpha,
                                   uint32_t* out, int32_t* nout, size_t lds_limit, hipStream_t stream) {
-  if (ncand < 0 || ncand > kBuildCandMax || g.R < 1 || g.R > kWave) return hipErrorInvalidValue;
+  if (ncand < 0 || ncand > kBuildCandMax || g.R < 1 || g.R > kWave || g.C < g.R) return hipErrorInvalidValue;
   if (PruneSmem::bytes(g.dp) > lds_limit) return hipErrorInvalidValue;
   return with_nc(g.dp, [&](auto nc) {
     hipLaunchKernelGGL(prune_one_kernel<decltype(nc)::value>, dim3(1), dim3(64), PruneSmem::bytes(g.dp), stream, g,

@@ -10,18 +10,24 @@ namespace gann {
 
 // Expanded nodes kept per build search and prune candidates per node.
 constexpr int kBuildPoolMax = 128;
-constexpr int kBuildCandMax = 192;
+constexpr int kBuildCandMax = 224;
 
 // Points resident in HBM with the graph under construction.
 struct BuildDev {
   const uint8_t* x;   // [n][dp] coordinates, rows zero padded to dp bytes
   const int32_t* xn;  // [n] squared norms
-  uint32_t* nbr;      // [n][R] out-neighbours, the first deg[i] valid
+  uint32_t* nbr;      // [n][C] out-neighbours, the first deg[i] valid
   uint32_t* deg;      // [n]
   int64_t n;
   int32_t dp;         // row bytes: 32, 64, 96, 128, 192 or 256
-  int32_t R;
+  int32_t R;          // degree a prune keeps
+  int32_t C;          // list capacity (R <= C <= kBuildSlackMax): reverse edges are
+                      // appended up to C before the list is pruned back to R
 };
+
+// List capacity with DiskANN's graph slack, ceil(1.3 R).
+constexpr int kBuildSlackMax = 84;
+constexpr int build_capacity(int R) { return (R * 13 + 9) / 10; }
 
 // Row bytes the builder stores for dim coordinates (0: dim unsupported).
 int build_row_bytes(int dim);
@@ -38,6 +44,13 @@ hipError_t launch_build_col_sums(const uint8_t* x, int64_t n, int dp, unsigned l
 // the caller).
 hipError_t launch_build_medoid(const uint8_t* x, int64_t n, int dim, int dp, const float* mean,
                                unsigned long long* best, hipStream_t stream);
+
+// Prunes every list longer than R back to R (the end of the build).
+hipError_t launch_build_final_prune(BuildDev g, float alpha, int32_t* queue, int cus, size_t lds_limit,
+                                    hipStream_t stream);
+
+// Copies the first R entries of every list into out ([n][R], device).
+hipError_t launch_build_compact(BuildDev g, uint32_t* out, hipStream_t stream);
 
 // Random initial graph: init_deg distinct random out-edges per node, no
 // self loops (the host builder's stream per node).

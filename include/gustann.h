@@ -210,9 +210,10 @@ int gann_pq_encode(const void* data, int64_t n, int32_t dim, int32_t dtype, cons
  * reference's own code.  Same steps as a sequential Vamana build: medoid
  * start, random initial graph of R/2 edges per node, a pass with alpha = 1
  * then one with `alpha`, each inserting every point in a seeded random order
- * by greedy search (list L), RobustPrune and reverse edges; points are
- * inserted in batches of at most max_batch (doubling from 1 in the first
- * pass) that see the graph as of the batch start.  data: [n][dim] on the
+ * by greedy search (list L), RobustPrune and reverse edges (lists grow to
+ * ceil(1.3 R) before a prune, DiskANN's slack, and are pruned back to R at
+ * the end); points are inserted in batches of at most max_batch (doubling
+ * from 1 in the first pass) that see the graph as of the batch start.  data: [n][dim] on the
  * host; out_nbr [n][R] and out_deg [n] on the host (row i: the first
  * out_deg[i] entries valid), *out_medoid the start node.  dim <= 256,
  * R <= 64, L <= 1024, n < 2^31 - 1.  verbose: progress lines on stderr. */
@@ -233,7 +234,7 @@ int gann_diag_gather_rows(const uint8_t* rows_dev, int64_t num_rows, int32_t row
 
 /* One RobustPrune of the graph builder on the device: point p of data
  * ([n][dim] uint8, host) over the candidate ids cand[0..ncand) (host,
- * ncand <= 192): candidates sorted by (exact squared L2 to p, id), repeated
+ * ncand <= 224): candidates sorted by (exact squared L2 to p, id), repeated
  * ids and p dropped, each kept candidate occludes a later one j when
  * d(p, j) / d(kept, j) > alpha; at most R kept, in order, into out (host,
  * R entries), their count into *nout.  No counterpart in the reference; it

@@ -89,10 +89,10 @@ def test_builder_and_encoder_argument_errors():
     off2 = np.array([0, 20, 40], np.int32)                  # chunks wider than 16 dims
     assert lib.gann_pq_encode(p(X2), 10, 40, 0, p(piv2), p(cen2), p(off2), 2, 0, p(codes)) == 6
     assert lib.gann_pq_encode(p(X), 10, 8, 7, p(piv), p(cen), p(off), 1, 0, p(codes)) == 1  # dtype
-    cand = np.zeros(193, np.uint32)
+    cand = np.zeros(225, np.uint32)
     out = np.zeros(64, np.uint32)
     k = ctypes.c_int32(0)
-    assert lib.gann_diag_robust_prune(p(X), 10, 8, 0, p(cand), 193, 1.2, 16, 0, p(out), ctypes.byref(k)) == 6
+    assert lib.gann_diag_robust_prune(p(X), 10, 8, 0, p(cand), 225, 1.2, 16, 0, p(out), ctypes.byref(k)) == 6
     assert lib.gann_diag_robust_prune(p(X), 10, 8, 10, p(cand), 4, 1.2, 16, 0, p(out), ctypes.byref(k)) == 1
     cand[0] = 99
     assert lib.gann_diag_robust_prune(p(X), 10, 8, 0, p(cand), 4, 1.2, 16, 0, p(out), ctypes.byref(k)) == 1

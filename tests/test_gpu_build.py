@@ -82,7 +82,7 @@ def test_prune_matches_restatement(dim, R, alpha, seed):
         # candidates mostly from p's neighbourhood, as after a search
         d = ((X.astype(np.int64) - X[p].astype(np.int64)) ** 2).sum(1)
         near = np.argsort(d, kind="stable")[:400]
-        nc = int(r.integers(0, 193)) if trial > 1 else 192
+        nc = int(r.integers(0, 225)) if trial > 1 else 224
         cand = r.choice(near, nc).astype(np.uint32)
         if nc > 3:
             cand[0], cand[1] = p, cand[2]
