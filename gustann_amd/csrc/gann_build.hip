@@ -458,49 +458,62 @@ __global__ __launch_bounds__(256) void build_reverse_kernel(BuildDev g, const un
                                                             const int32_t* __restrict__ n_seg, float alpha,
                                                             int32_t* __restrict__ queue) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
+  constexpr int kGrab = 8;  // runs taken per queue access
   const int lane = lane_id();
   const PruneSmem S(smem_raw + (size_t)(threadIdx.x >> 6) * PruneSmem::bytes(g.dp));
   const int ns = __builtin_amdgcn_readfirstlane(*n_seg);
   for (;;) {
-    int s = 0;
-    if (lane == 0) s = atomicAdd(queue, 1);
-    s = __builtin_amdgcn_readfirstlane(__shfl(s, 0, kWave));
-    if (s >= ns) break;
-    const int64_t a = seg_start[s];
-    const int64_t b = s + 1 < ns ? (int64_t)seg_start[s + 1] : npairs;
-    const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(pairs[a] >> 32));
-    if ((int64_t)v >= g.n) continue;  // the run of unused slots
-    const int dv = __builtin_amdgcn_readfirstlane((int)min(g.deg[v], (uint32_t)g.C));
-    for (int e = lane; e < dv; e += kWave) S.outl[e] = g.nbr[(int64_t)v * g.C + e];
-    wave_sync();
-    // new sources: not listed yet, at most kBuildCandMax - dv of them
-    const int room = kBuildCandMax - dv;
-    int m_new = 0;
-    for (int64_t t = a; t < b && m_new < room; t += kWave) {
-      const int64_t i = t + lane;
-      const uint32_t src = i < b ? (uint32_t)pairs[i] : 0xffffffffu;
-      bool ok = i < b && src != v && (int64_t)src < g.n;
-      for (int e = 0; e < dv; ++e) ok = ok && S.outl[e] != src;
-      const uint64_t mask = ballot64(ok);
-      const int pos = m_new + rank_below(mask);
-      if (ok && pos < room) S.cid[pos] = src;
-      m_new = min(m_new + (int)__popcll(mask), room);
-    }
-    wave_sync();
-    if (dv + m_new <= g.C) {
-      for (int e = lane; e < m_new; e += kWave) g.nbr[(int64_t)v * g.C + dv + e] = S.cid[e];
-      if (lane == 0) g.deg[v] = (uint32_t)(dv + m_new);
-    } else {
-      uint32_t w[4 * NC];
-      uniform_row<NC>(g.x, g.dp, v, w);
-      const int32_t nv = __builtin_amdgcn_readfirstlane(g.xn[v]);
-      for (int c = lane; c < dv + m_new; c += kWave) {
-        const uint32_t id = c < dv ? S.outl[c] : S.cid[c - dv];
-        S.keys[c] = make_key(sq_dist(nv, g.xn[id], row_dot<NC>(w, g.x + (int64_t)id * g.dp)), id);
+    int s0 = 0;
+    if (lane == 0) s0 = atomicAdd(queue, kGrab);
+    s0 = __builtin_amdgcn_readfirstlane(__shfl(s0, 0, kWave));
+    if (s0 >= ns) break;
+    for (int s = s0; s < min(s0 + kGrab, ns); ++s) {
+      const int64_t a = seg_start[s];
+      const int64_t b = s + 1 < ns ? (int64_t)seg_start[s + 1] : npairs;
+      const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(pairs[a] >> 32));
+      if ((int64_t)v >= g.n) continue;  // the run of unused slots
+      const int dv = __builtin_amdgcn_readfirstlane((int)min(g.deg[v], (uint32_t)g.C));
+      // the current list, one entry per lane and register (C <= 2 * 64)
+      const uint32_t l0 = lane < dv ? g.nbr[(int64_t)v * g.C + lane] : 0xffffffffu;
+      const uint32_t l1 = lane + kWave < dv ? g.nbr[(int64_t)v * g.C + kWave + lane] : 0xffffffffu;
+      // new sources: not listed yet, at most kBuildCandMax - dv of them
+      const int room = kBuildCandMax - dv;
+      int m_new = 0;
+      for (int64_t t = a; t < b && m_new < room; t += kWave) {
+        const int64_t i = t + lane;
+        const uint32_t src = i < b ? (uint32_t)pairs[i] : 0xffffffffu;
+        uint64_t cand = ballot64(i < b && src != v && (int64_t)src < g.n);
+        uint64_t keep = 0;
+        while (cand) {
+          const int j = (int)__builtin_ctzll(cand);
+          cand &= cand - 1;
+          const uint32_t sj = (uint32_t)__builtin_amdgcn_readlane((int)src, j);
+          if (!ballot64(l0 == sj || l1 == sj)) keep |= 1ull << j;
+        }
+        const bool ok = (keep >> lane) & 1;
+        const int pos = m_new + rank_below(keep);
+        if (ok && pos < room) S.cid[pos] = src;
+        m_new = min(m_new + (int)__popcll(keep), room);
       }
-      prune_wave<NC>(g, v, dv + m_new, alpha, S);
+      wave_sync();
+      if (dv + m_new <= g.C) {
+        for (int e = lane; e < m_new; e += kWave) g.nbr[(int64_t)v * g.C + dv + e] = S.cid[e];
+        if (lane == 0) g.deg[v] = (uint32_t)(dv + m_new);
+      } else {
+        uint32_t w[4 * NC];
+        uniform_row<NC>(g.x, g.dp, v, w);
+        const int32_t nv = __builtin_amdgcn_readfirstlane(g.xn[v]);
+        if (lane < dv) S.outl[lane] = l0;
+        if (lane + kWave < dv) S.outl[kWave + lane] = l1;
+        wave_sync();
+        for (int c = lane; c < dv + m_new; c += kWave) {
+          const uint32_t id = c < dv ? S.outl[c] : S.cid[c - dv];
+          S.keys[c] = make_key(sq_dist(nv, g.xn[id], row_dot<NC>(w, g.x + (int64_t)id * g.dp)), id);
+        }
+        prune_wave<NC>(g, v, dv + m_new, alpha, S);
+      }
+      wave_sync();
     }
-    wave_sync();
   }
 }
 
