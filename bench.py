@@ -328,7 +328,14 @@ def bench_gather(args):
     """The ADC microbenchmark's memory access alone (gann_diag_gather_rows):
     the same 100M x 32-byte codes and 10k x 4096 ids (same seeds as the adc
     workload), every row read and folded, no LUT and no arithmetic.  Its time
-    is the ceiling of the ADC scan on this access pattern."""
+    is the ceiling of the ADC scan on this access pattern.
+
+    --gather-order reorders the same requests before timing: "band:B" groups
+    all requests by id >> B (band-major, the order inside a band kept), i.e.
+    every query's rows of one 2^B-row band of the table are read before the
+    next band's; "sorted" sorts all requests by id.  They measure how much of
+    the random-order time is line re-fetches that an order sharing lines
+    across queries would save."""
     import ctypes as C
     import torch
     from gustann_amd import _native as N
@@ -339,6 +346,18 @@ def bench_gather(args):
     g.manual_seed(7)
     codes = torch.randint(0, 256, (N_, M), dtype=torch.uint8, device=dev, generator=g)
     ids = torch.randint(0, N_, (nq, S), dtype=torch.int32, device=dev, generator=g)
+    order = args.gather_order
+    if order == "sorted":
+        ids = torch.sort(ids.view(-1)).values.view(nq, S).contiguous()
+    elif order.startswith("band:"):
+        shift = int(order.split(":", 1)[1])
+        if not 0 <= shift < 31:
+            raise SystemExit("--gather-order band:B needs 0 <= B < 31")
+        perm = torch.argsort((ids.view(-1) >> shift).to(torch.int64), stable=True)
+        ids = ids.view(-1)[perm].view(nq, S).contiguous()
+        del perm
+    elif order != "random":
+        raise SystemExit("--gather-order is random, sorted or band:B")
     out = torch.empty((nq, S), dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
     lib = N.hip_lib()
@@ -358,7 +377,7 @@ def bench_gather(args):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
     rows = nq * S
-    return {"workload": "gather_rows_adc_pattern", "rows": rows, "row_bytes": M,
+    return {"workload": "gather_rows_adc_pattern", "order": order, "rows": rows, "row_bytes": M,
             "ms_per_launch": ms, "rows_per_s": rows / (ms / 1e3),
             "row_bytes_GBps": rows * M / (ms / 1e3) / 1e9,
             "line_bytes_GBps": rows * 128 / (ms / 1e3) / 1e9}
@@ -394,6 +413,8 @@ def main():
     ap.add_argument("--workload", choices=["adc", "search", "copy", "knn", "gather"], default="adc")
     ap.add_argument("--knn-k", type=int, default=100)
     ap.add_argument("--copy-bytes", type=int, default=1 << 31)
+    ap.add_argument("--gather-order", default="random",
+                    help="gather workload: random (the ADC pattern), sorted, or band:B")
     ap.add_argument("--nq", type=int, default=10000)
     ap.add_argument("--ids-per-query", type=int, default=4096)
     ap.add_argument("--num-codes", type=int, default=100_000_000)
