@@ -364,11 +364,16 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
 // (src/impl/pure_mem.cuh:306-308), so the distances are bit-identical to the
 // LUT path while a query needs only its list, query vector and top-k in LDS.
 //
-// Pivot row c (the dim floats of code c) starts at byte c*4*dim + (c & 0xF0):
-// each run of 16 rows sits 16 bytes further than the previous one, which
-// spreads the lanes of a wave (random rows, same chunk) over the LDS banks
-// for 240 bytes of padding, and a chunk's offset inside its row stays a
+// Pivot row c (the dim floats of code c) starts at byte c*(4*dim + 16): the
+// 16 bytes of padding per row move consecutive rows 4 banks apart, which
+// spreads the lanes of a wave (random rows, same chunk) over the LDS banks;
+// a row address is one 24-bit multiply of the code byte (the compiler folds
+// the byte select into it), and a chunk's offset inside its row stays a
 // compile-time immediate of the LDS read.
+
+// Row stride of the shared-codebook pivot layout for rows of `row_bytes`
+// bytes of floats.
+__host__ __device__ constexpr uint32_t cb_stride(int row_bytes) { return (uint32_t)row_bytes + 16u; }
 
 struct CbSmem {
   // per-wave bytes: list (L) | list scratch | top-k d, top-k id (LDS only
@@ -378,16 +383,18 @@ struct CbSmem {
     size_t b = (size_t)L * 8 + (size_t)list_scratch_words(L) * 4 + (k > kWave ? (size_t)k * 8 : 0);
     return (b + 15) & ~(size_t)15;
   }
-  static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * dim * 4 + 240; }
+  static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * cb_stride(4 * dim); }
 };
 
 // LDS bytes of the first g groups of 8 chunks of W dims, in the cb_row layout.
 __host__ __device__ constexpr size_t split_pivot_bytes(int g, int W) {
-  return g > 0 ? (size_t)kPivots * g * 8 * W * 4 + 240 : 0;
+  return g > 0 ? (size_t)kPivots * cb_stride(g * 8 * W * 4) : 0;
 }
 
-__device__ __forceinline__ uint32_t cb_row(uint32_t c, uint32_t rowb) {
-  return __umul24(c, rowb) + (c & 0xF0u);
+// Byte offset of pivot row c in a table whose rows are `stride` bytes apart
+// (stride = cb_stride(bytes of the row's floats)).
+__device__ __forceinline__ uint32_t cb_row(uint32_t c, uint32_t stride) {
+  return __umul24(c, stride);
 }
 
 // q - mu of every query (src/impl/pq.cuh:22-24), read back with uniform
@@ -423,7 +430,7 @@ struct PivotVec<2> {
 };
 
 // ADC distance of one code row from the pivots in LDS (piv: byte base of the
-// table, rowb = 4*dim).  The pivot reads of 8 chunks are issued together;
+// table, rowb = cb_stride(4*dim)).  The pivot reads of 8 chunks are issued together;
 // q - mu is read 8 chunks at a time with uniform loads from qs, whose
 // address is made opaque per group so the compiler does not keep all of it
 // in scalar registers across expansions.
@@ -444,7 +451,7 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
         PV p[8];
         const bool from_lds = 2 * k + h < kSplitG;  // compile-time
         const uint8_t* base = from_lds ? pivl : piv;
-        const uint32_t stride = from_lds ? (uint32_t)(kSplitG * 8 * W * 4) : rowb;
+        const uint32_t stride = from_lds ? cb_stride(kSplitG * 8 * W * 4) : rowb;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
           const int bb = 8 * h + b;
@@ -499,7 +506,7 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
                                                          const float* __restrict__ qs_all) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
-  const uint32_t rowb = 4u * (uint32_t)dim;
+  const uint32_t rowb = cb_stride(4 * dim);
   const uint8_t* piv;
   size_t lists_at = 0;
   if constexpr (kGP) {
@@ -509,7 +516,7 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
       constexpr int per_row = kSplitG * 8 * W;
       for (int idx = threadIdx.x; idx < kPivots * per_row; idx += blockDim.x) {
         const int c = idx / per_row, i = idx - c * per_row;
-        *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, per_row * 4) + 4 * i) = pq.pivots[c * dim + i];
+        *reinterpret_cast<float*>(smem_raw + cb_row((uint32_t)c, cb_stride(per_row * 4)) + 4 * i) = pq.pivots[c * dim + i];
       }
       __syncthreads();
       lists_at = split_pivot_bytes(kSplitG, W);
@@ -609,7 +616,7 @@ __global__ __launch_bounds__(1024) void search_beam_kernel(IndexDev ix, PQDev pq
                                                            const float* __restrict__ qs_all) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
-  const uint32_t rowb = 4u * (uint32_t)dim;
+  const uint32_t rowb = cb_stride(4 * dim);
   const uint8_t* piv;
   size_t lists_at = 0;
   if constexpr (kGP) {
@@ -1017,11 +1024,11 @@ int search_cb_split_groups(int M, int chunk_w) {
 size_t search_cb_pivot_bytes(int dim) { return CbSmem::pivot_bytes(dim); }
 
 void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out) {
-  const uint32_t rowb = 4u * (uint32_t)dim;
+  const uint32_t rowb = cb_stride(4 * dim);
   std::fill(out, out + CbSmem::pivot_bytes(dim), (uint8_t)0);
   for (uint32_t c = 0; c < (uint32_t)kPivots; ++c)
     std::copy(reinterpret_cast<const uint8_t*>(pivots + (size_t)c * dim),
-              reinterpret_cast<const uint8_t*>(pivots + (size_t)(c + 1) * dim), out + c * rowb + (c & 0xF0u));
+              reinterpret_cast<const uint8_t*>(pivots + (size_t)(c + 1) * dim), out + (size_t)c * rowb);
 }
 
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
