@@ -85,6 +85,13 @@ struct ListPlan {
 // Ranks each lane's candidate (lanes < deg) in the list, drops those whose id
 // is listed already, sorts the rest with their ranks into lanes 0..n_nd-1
 // (an inserted entry's position is then rank + lane) and picks the next node.
+//
+// A candidate ranked at L (the list is full and every entry orders below it)
+// is dropped with the duplicates before the sort: it could only land at a
+// position >= L, and it orders after every inserted entry, so the others'
+// positions are unchanged.  Most expansions of a converged search have no
+// candidate left (about four in five at L = 448 on a 128-d uint8 mixture)
+// and skip the sort.
 __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t key, int deg,
                                               int sz, int fu) {
   const int lane = lane_id();
@@ -93,8 +100,8 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
   uint32_t r = (uint32_t)list_rank(A, sz, key, active);
   // a candidate whose id is listed already sits at its lower bound
   const bool dup = active && (int)r < sz && entry_id(A[r]) == entry_id(key);
-  if (!active || dup) key = ~(uint64_t)0;  // never a real key: ids are < 2^31 - 1
-  wave_sort64_kv(key, r);
+  if (!active || dup || (int)r >= L) key = ~(uint64_t)0;  // never a real key: ids are < 2^31 - 1
+  if (ballot64(key != ~(uint64_t)0) != 0) wave_sort64_kv(key, r);  // uniform branch
   ListPlan P;
   P.nkey = key;
   P.n_nd = __popcll(ballot64(key != ~(uint64_t)0));
