@@ -1,0 +1,139 @@
+"""The device list update (gustann_amd/csrc/gann_list.hpp list_plan /
+list_apply) restated in Python, against the reference's formulation
+(src/impl/pure_mem.cuh:350-419: merge with an equal new item after the old
+one, cap at 2L, drop every entry whose id equals its predecessor's, cap at
+L, take the first unvisited entry) on random update sequences.
+
+The device form ranks each candidate in the list, drops candidates whose id
+sits at their lower bound (duplicates) and candidates ranked at L (the list
+is full and all of it orders below them), skips the sort when none is left,
+places the k-th survivor in key order at rank + k, keeps the first L
+entries, and picks min(new position of the old first-unvisited entry,
+position of the first inserted entry).  Keys are the kernel's 64-bit
+encoding: bits(dist) << 32 | id << 1 | visited.
+"""
+import bisect
+import random
+
+import pytest
+
+VISITED = 1
+
+
+def key_of(d, i):
+    return (d << 32) | (i << 1)
+
+
+def ident(k):
+    return (k >> 1) & 0x7FFFFFFF
+
+
+def reference_update(lst, cands, L):
+    """Merge, 2L cap, adjacent-id dedup, L cap (pure_mem.cuh:350-419)."""
+    merged = sorted([(k & ~VISITED, 0, k) for k in lst] + [(c, 1, c) for c in cands])
+    merged = [t[2] for t in merged][:2 * L]
+    out = []
+    for k in merged:
+        if out and ident(out[-1]) == ident(k):
+            continue  # keeps the earlier (pre-existing) copy
+        out.append(k)
+    return out[:L]
+
+
+def device_update(lst, cands, L, fu):
+    """list_plan + list_apply of gann_list.hpp; returns (new list, next
+    position or -1, the count of inserted entries, whether the sort ran)."""
+    sz = len(lst)
+    fu_entry = lst[fu] if fu < sz else None
+    surv = []
+    for c in cands:
+        r = bisect.bisect_left(lst, c)           # entries ordered below c
+        dup = r < sz and ident(lst[r]) == ident(c)
+        if not dup and r < L:
+            surv.append((c, r))
+    sorted_run = bool(surv)
+    surv.sort()
+    nsz = min(sz + len(surv), L)
+    pos = [r + e for e, (c, r) in enumerate(surv)]
+    new = [None] * nsz
+    marked = {p: c for p, (c, _) in zip(pos, surv) if p < nsz}
+    nb = 0
+    for j in range(nsz):                         # output j: inserted or old j - nb
+        if j in marked:
+            new[j] = marked[j]
+            nb += 1
+        else:
+            new[j] = lst[j - nb]
+    p0 = pos[0] if surv else None
+    fu_new = None
+    if fu < sz:
+        fu_new = fu + sum(1 for (c, r) in surv if r <= fu)
+    cands_pos = [x for x in (fu_new, p0) if x is not None]
+    cand = min(cands_pos) if cands_pos else None
+    if cand is None or cand >= nsz:
+        return new, -1, len(surv), sorted_run
+    sel = fu_entry if cand == fu_new else surv[0][0]
+    assert new[cand] == sel
+    return new, cand, len(surv), sorted_run
+
+
+def first_unvisited(lst):
+    for j, k in enumerate(lst):
+        if not k & VISITED:
+            return j
+    return len(lst)
+
+
+@pytest.mark.parametrize("L", [1, 4, 17, 64, 100, 300])
+def test_device_update_equals_reference_merge(L):
+    rng = random.Random(1000 + L)
+    skipped = ran = 0
+    for seq in range(60 if L < 100 else 25):
+        ids = rng.sample(range(1, 5000), 600)
+        dist = {i: rng.randrange(0, 40) for i in ids}  # few distinct values: many ties
+        ref, dev = [], []
+        fu = 0
+        for step in range(80):
+            deg = rng.randrange(0, 65)
+            nbrs = rng.sample(ids, deg)                  # distinct ids, as in a record
+            cands = [key_of(dist[i], i) for i in nbrs]
+            ref = reference_update(ref, cands, L)
+            dev, cand, n, sorted_run = device_update(dev, cands, L, fu)
+            assert dev == ref, (L, seq, step)
+            # the reference's next node: the first unvisited entry below L
+            nxt = first_unvisited(ref)
+            assert (cand if cand >= 0 else len(ref)) == nxt, (L, seq, step)
+            skipped += not sorted_run
+            ran += sorted_run
+            if cand < 0:
+                break
+            ref[nxt] |= VISITED
+            dev[cand] |= VISITED
+            fu = first_unvisited(dev)
+    assert ran > 0
+    if L >= 17:
+        assert skipped > 0  # the no-survivor path was exercised
+
+
+def test_rank_at_L_is_never_inserted():
+    """A full list and candidates that order after all of it: nothing is
+    inserted, the sort is skipped, and the reference keeps the list too."""
+    L = 8
+    lst = [key_of(d, 100 + d) for d in range(L)]
+    cands = [key_of(50 + j, 500 + j) for j in range(10)]
+    new, cand, n, sorted_run = device_update(lst, cands, L, 0)
+    assert n == 0 and not sorted_run and new == lst and cand == 0
+    assert reference_update(lst, cands, L) == lst
+
+
+def test_duplicate_of_the_last_entry_is_dropped():
+    """The candidate equal to the unvisited last entry (same id, same
+    distance) is a duplicate, not an insertion; a visited copy orders one
+    above the fresh key and is found at the lower bound too."""
+    L = 4
+    lst = [key_of(d, 10 + d) for d in range(L)]
+    for last in (lst[-1], lst[-1] | VISITED):
+        cur = lst[:-1] + [last]
+        new, _, n, _ = device_update(cur, [key_of(L - 1, 10 + L - 1)], L, 0)
+        assert n == 0 and new == cur
+        assert reference_update(cur, [key_of(L - 1, 10 + L - 1)], L) == cur
