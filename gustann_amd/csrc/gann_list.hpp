@@ -101,10 +101,11 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
   // a candidate whose id is listed already sits at its lower bound
   const bool dup = active && (int)r < sz && entry_id(A[r]) == entry_id(key);
   if (!active || dup || (int)r >= L) key = ~(uint64_t)0;  // never a real key: ids are < 2^31 - 1
-  if (ballot64(key != ~(uint64_t)0) != 0) wave_sort64_kv(key, r);  // uniform branch
+  const uint64_t live = ballot64(key != ~(uint64_t)0);
+  if (live != 0) wave_sort64_kv(key, r);  // uniform branch; the sort keeps the count
   ListPlan P;
   P.nkey = key;
-  P.n_nd = __popcll(ballot64(key != ~(uint64_t)0));
+  P.n_nd = __popcll(live);
   P.p = (int)r + lane;
   P.p0 = P.n_nd ? __builtin_amdgcn_readlane((int)r, 0) : INT_MAX;
   P.nsz = min(sz + P.n_nd, L);
