@@ -436,7 +436,21 @@ struct PivotVec<2> {
 // in scalar registers across expansions.
 // kSplitG > 0: groups of 8 chunks below kSplitG come from the partial
 // table pivl in LDS (rows of kSplitG * 8 * W floats), the others from piv.
-template <int W, int MW, int kSplitG = 0>
+// The partial table is addressed from pivl: with its rows read from LDS
+// address 0 the compiler keeps more reads in flight and spills registers in
+// those kernels (1024-lane workgroups cap them at 128 VGPRs).
+// kPivLds: piv is the whole table in LDS, at the beginning of the dynamic
+// LDS, which is LDS address 0: the kernels that call this declare no static
+// LDS, and their launchers check that with hipFuncGetAttributes.  Reading LDS rows by their address from 0 leaves the
+// row address as one 24-bit multiply of the code byte (the compiler folds the
+// byte select into it); an offset from the dynamic LDS symbol costs a second
+// VALU operation per chunk.
+template <typename PV>
+__device__ __forceinline__ PV lds_at(uint32_t a) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) PV*>((size_t)a);
+}
+
+template <int W, int MW, int kSplitG = 0, bool kPivLds = false>
 __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uint32_t rowb,
                                         const PQDev& pq, const CodeRow<MW>& row,
                                         const uint8_t* crow, const uint8_t* pivl = nullptr) {
@@ -450,13 +464,16 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
       for (int h = 0; h < 2; ++h) {
         PV p[8];
         const bool from_lds = 2 * k + h < kSplitG;  // compile-time
-        const uint8_t* base = from_lds ? pivl : piv;
         const uint32_t stride = from_lds ? cb_stride(kSplitG * 8 * W * 4) : rowb;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
           const int bb = 8 * h + b;
           const uint32_t c = (ws[bb >> 2] >> (8 * (bb & 3))) & 0xffu;
-          p[b] = *reinterpret_cast<const PV*>(base + cb_row(c, stride) + (16 * k + bb) * W * 4);
+          const uint32_t off = cb_row(c, stride) + (16 * k + bb) * W * 4;
+          if (kPivLds)
+            p[b] = lds_at<PV>(off);  // the whole table at LDS address 0
+          else
+            p[b] = *reinterpret_cast<const PV*>((from_lds ? pivl : piv) + off);
         }
         // uniform address in the constant address space: scalar loads
         uint64_t qa = (uint64_t)(qs + (16 * k + 8 * h) * W);
@@ -564,7 +581,7 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
         CodeRow<MW> row;
         const uint8_t* crow = pq.codes + (int64_t)cur.v * M;
         row.load(crow, M);
-        key = make_key(cb_adc<W, MW, kSplitG>(piv, qs, rowb, pq, row, crow, smem_raw), cur.v);
+        key = make_key(cb_adc<W, MW, kSplitG, !kGP>(piv, qs, rowb, pq, row, crow, smem_raw), cur.v);
       }
       const float du = cur.l2(qv, dim);
       const ListPlan P = list_plan(A, L, key, deg, sz, fu);
@@ -679,7 +696,7 @@ __global__ __launch_bounds__(1024) void search_beam_kernel(IndexDev ix, PQDev pq
           uint64_t key = ~(uint64_t)0;
           if (lane < deg) {
             const uint8_t* crow = pq.codes + (int64_t)rec[b].v * M;
-            key = make_key(cb_adc<W, MW>(piv, qs, rowb, pq, rows[b & 1], crow), rec[b].v);
+            key = make_key(cb_adc<W, MW, 0, !kGP>(piv, qs, rowb, pq, rows[b & 1], crow), rec[b].v);
           }
           const float du = rec[b].l2(qv, dim);
           const ListPlan P = list_plan(A, L, key, deg, sz, fu);
@@ -1031,6 +1048,27 @@ void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out) {
               reinterpret_cast<const uint8_t*>(pivots + (size_t)(c + 1) * dim), out + (size_t)c * rowb);
 }
 
+namespace {
+// The shared-codebook kernels with the whole pivot table in LDS address it
+// from LDS address 0 (lds_at), which is where the dynamic LDS starts only
+// when the kernel has no static LDS: refuse the launch otherwise (checked for
+// every form, so that none gains static LDS unnoticed).
+hipError_t check_dynamic_lds_at_zero(const void* fn) {
+  hipFuncAttributes a{};
+  const hipError_t e = hipFuncGetAttributes(&a, fn);
+  if (e != hipSuccess) return e;
+  return a.sharedSizeBytes == 0 ? hipSuccess : hipErrorInvalidDeviceFunction;
+}
+
+template <class K, class F>
+hipError_t launch_checked(K* fn, F&& launch) {
+  const hipError_t e = check_dynamic_lds_at_zero(reinterpret_cast<const void*>(fn));
+  if (e != hipSuccess) return e;
+  launch();
+  return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
@@ -1057,22 +1095,28 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
         constexpr bool kCanSplit = MWv > 0 && (Wv == 2 || Wv == 4);
         constexpr int kSplit = kCanSplit ? 2 * MWv - 1 : 0, kHalf = kCanSplit ? MWv : 0;
         if (global_pivots && lds_groups > 0 && kCanSplit && lds_groups == kSplit)
-          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kSplit>), dim3(blocks), dim3(waves * kWave),
-                             smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
-                             queue, qs_all);
-        else if (global_pivots && lds_groups > 0 && kCanSplit && lds_groups == kHalf)
-          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kHalf>), dim3(blocks), dim3(waves * kWave),
-                             smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
-                             queue, qs_all);
-        else if (global_pivots)
-          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true>), dim3(blocks), dim3(waves * kWave), smem,
-                             stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
-                             qs_all);
-        else
+          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kSplit>, [&] {
+            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kSplit>), dim3(blocks), dim3(waves * kWave),
+                               smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
+                               queue, qs_all);
+          });
+        if (global_pivots && lds_groups > 0 && kCanSplit && lds_groups == kHalf)
+          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kHalf>, [&] {
+            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kHalf>), dim3(blocks), dim3(waves * kWave),
+                               smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
+                               queue, qs_all);
+          });
+        if (global_pivots)
+          return launch_checked(&search_cb_kernel<T, MWv, Wv, true>, [&] {
+            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true>), dim3(blocks), dim3(waves * kWave), smem,
+                               stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
+                               qs_all);
+          });
+        return launch_checked(&search_cb_kernel<T, MWv, Wv, false>, [&] {
           hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, false>), dim3(blocks), dim3(waves * kWave), smem,
                              stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
                              qs_all);
-        return hipGetLastError();
+        });
       });
     });
   };
@@ -1100,17 +1144,18 @@ hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, co
     using T = decltype(t);
     return with_mw(pq.M, [&](auto mw) {
       return with_w(pq.chunk_w, [&](auto w) {
+        constexpr int MWv = decltype(mw)::value, Wv = decltype(w)::value, KPv = decltype(kp)::value;
         if (global_pivots)
-          hipLaunchKernelGGL(
-              (search_beam_kernel<T, decltype(mw)::value, decltype(w)::value, decltype(kp)::value, true>),
-              dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries, topk, L, bw,
-              nns, dists, found, n_exp, n_adc, queue, qs_all);
-        else
-          hipLaunchKernelGGL(
-              (search_beam_kernel<T, decltype(mw)::value, decltype(w)::value, decltype(kp)::value, false>),
-              dim3(blocks), dim3(waves * kWave), smem, stream, ix, pq, q, nq, entries, topk, L, bw,
-              nns, dists, found, n_exp, n_adc, queue, qs_all);
-        return hipGetLastError();
+          return launch_checked(&search_beam_kernel<T, MWv, Wv, KPv, true>, [&] {
+            hipLaunchKernelGGL((search_beam_kernel<T, MWv, Wv, KPv, true>), dim3(blocks), dim3(waves * kWave),
+                               smem, stream, ix, pq, q, nq, entries, topk, L, bw, nns, dists, found, n_exp,
+                               n_adc, queue, qs_all);
+          });
+        return launch_checked(&search_beam_kernel<T, MWv, Wv, KPv, false>, [&] {
+          hipLaunchKernelGGL((search_beam_kernel<T, MWv, Wv, KPv, false>), dim3(blocks), dim3(waves * kWave),
+                             smem, stream, ix, pq, q, nq, entries, topk, L, bw, nns, dists, found, n_exp,
+                             n_adc, queue, qs_all);
+        });
       });
     });
   };
