@@ -436,9 +436,10 @@ struct PivotVec<2> {
 // in scalar registers across expansions.
 // kSplitG > 0: groups of 8 chunks below kSplitG come from the partial
 // table pivl in LDS (rows of kSplitG * 8 * W floats), the others from piv.
-// The partial table is addressed from pivl: with its rows read from LDS
-// address 0 the compiler keeps more reads in flight and spills registers in
-// those kernels (1024-lane workgroups cap them at 128 VGPRs).
+// kSplitLds: read the partial table from LDS address 0 as well (pivl is the
+// start of the dynamic LDS).  The compiler then keeps more reads in flight;
+// with 8 rerank slots per lane that spills registers (1024-lane workgroups
+// cap a kernel at 128 VGPRs), so only the 4-slot kernels (dim <= 128) do.
 // kPivLds: piv is the whole table in LDS, at the beginning of the dynamic
 // LDS, which is LDS address 0: the kernels that call this declare no static
 // LDS, and their launchers check that with hipFuncGetAttributes.  Reading LDS rows by their address from 0 leaves the
@@ -450,7 +451,7 @@ __device__ __forceinline__ PV lds_at(uint32_t a) {
   return *reinterpret_cast<const __attribute__((address_space(3))) PV*>((size_t)a);
 }
 
-template <int W, int MW, int kSplitG = 0, bool kPivLds = false>
+template <int W, int MW, int kSplitG = 0, bool kPivLds = false, bool kSplitLds = false>
 __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uint32_t rowb,
                                         const PQDev& pq, const CodeRow<MW>& row,
                                         const uint8_t* crow, const uint8_t* pivl = nullptr) {
@@ -470,8 +471,8 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
           const int bb = 8 * h + b;
           const uint32_t c = (ws[bb >> 2] >> (8 * (bb & 3))) & 0xffu;
           const uint32_t off = cb_row(c, stride) + (16 * k + bb) * W * 4;
-          if (kPivLds)
-            p[b] = lds_at<PV>(off);  // the whole table at LDS address 0
+          if (kPivLds || (from_lds && kSplitLds))
+            p[b] = lds_at<PV>(off);  // a table at LDS address 0 (whole, or partial)
           else
             p[b] = *reinterpret_cast<const PV*>((from_lds ? pivl : piv) + off);
         }
@@ -510,7 +511,8 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
 // kGP: the pivot table is read from pq.piv_cb (HBM, through the caches)
 // instead of a copy in LDS, which then holds only the per-wave lists: the
 // form for large L, where lists beside a 128 KB table leave few waves.
-template <typename T, int MW, int W, bool kGP, int kSplitG = 0>
+// KP: rerank coordinates per lane (dim <= 32 * KP).
+template <typename T, int MW, int W, bool kGP, int kSplitG = 0, int KP = kMaxDimRegs>
 __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
                                                          const float* __restrict__ q, int nq,
                                                          const int32_t* __restrict__ entries,
@@ -564,10 +566,10 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
     qi = __builtin_amdgcn_readfirstlane(__shfl(qi, 0, kWave));
     if (qi >= nq) break;
     int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
-    RecRegs<T, kMaxDimRegs> cur;
+    RecRegs<T, KP> cur;
     if (u >= 0) cur.load(ix, u);
     const float* qs = qs_all + (int64_t)qi * dim;  // q - mu, uniform reads
-    float qv[kMaxDimRegs];
+    float qv[KP];
     restored_query_regs(q + (int64_t)qi * dim, pq.centroid, dim, qv);
     int sz = 0, fu = 0;
     TopK top(td, ti, topk);
@@ -581,13 +583,13 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
         CodeRow<MW> row;
         const uint8_t* crow = pq.codes + (int64_t)cur.v * M;
         row.load(crow, M);
-        key = make_key(cb_adc<W, MW, kSplitG, !kGP>(piv, qs, rowb, pq, row, crow, smem_raw), cur.v);
+        key = make_key(cb_adc<W, MW, kSplitG, !kGP, (KP <= 4)>(piv, qs, rowb, pq, row, crow, smem_raw), cur.v);
       }
       const float du = cur.l2(qv, dim);
       const ListPlan P = list_plan(A, L, key, deg, sz, fu);
       const int32_t next =
           __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)entry_id(P.sel) : -1);
-      RecRegs<T, kMaxDimRegs> nxt;
+      RecRegs<T, KP> nxt;
       if (next >= 0) nxt.load(ix, next);
       fu = list_apply(A, BM, P);
       sz = P.nsz;
@@ -1087,41 +1089,48 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
                      pq.centroid, n, ix.dim, qs_all);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  auto go = [&](auto t) {
+  auto go = [&](auto t, auto kp) {
     using T = decltype(t);
+    constexpr int KPv = decltype(kp)::value;
     return with_mw(pq.M, [&](auto mw) {
       return with_w(pq.chunk_w, [&](auto w) {
         constexpr int MWv = decltype(mw)::value, Wv = decltype(w)::value;
         constexpr bool kCanSplit = MWv > 0 && (Wv == 2 || Wv == 4);
         constexpr int kSplit = kCanSplit ? 2 * MWv - 1 : 0, kHalf = kCanSplit ? MWv : 0;
         if (global_pivots && lds_groups > 0 && kCanSplit && lds_groups == kSplit)
-          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kSplit>, [&] {
-            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kSplit>), dim3(blocks), dim3(waves * kWave),
+          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kSplit, KPv>, [&] {
+            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kSplit, KPv>), dim3(blocks), dim3(waves * kWave),
                                smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
                                queue, qs_all);
           });
         if (global_pivots && lds_groups > 0 && kCanSplit && lds_groups == kHalf)
-          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kHalf>, [&] {
-            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kHalf>), dim3(blocks), dim3(waves * kWave),
+          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kHalf, KPv>, [&] {
+            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kHalf, KPv>), dim3(blocks), dim3(waves * kWave),
                                smem, stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc,
                                queue, qs_all);
           });
         if (global_pivots)
-          return launch_checked(&search_cb_kernel<T, MWv, Wv, true>, [&] {
-            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true>), dim3(blocks), dim3(waves * kWave), smem,
+          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, 0, KPv>, [&] {
+            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, 0, KPv>), dim3(blocks), dim3(waves * kWave), smem,
                                stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
                                qs_all);
           });
-        return launch_checked(&search_cb_kernel<T, MWv, Wv, false>, [&] {
-          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, false>), dim3(blocks), dim3(waves * kWave), smem,
+        return launch_checked(&search_cb_kernel<T, MWv, Wv, false, 0, KPv>, [&] {
+          hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, false, 0, KPv>), dim3(blocks), dim3(waves * kWave), smem,
                              stream, ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
                              qs_all);
         });
       });
     });
   };
-  if (dtype == 0) return go(uint8_t{});
-  return go(float{});
+  // 4 rerank coordinates per lane cover dim <= 128 (fewer registers and no
+  // idle rerank slots); larger dims take kMaxDimRegs
+  const bool small = ix.dim <= 128;
+  if (dtype == 0)
+    return small ? go(uint8_t{}, std::integral_constant<int, 4>{})
+                 : go(uint8_t{}, std::integral_constant<int, kMaxDimRegs>{});
+  return small ? go(float{}, std::integral_constant<int, 4>{})
+               : go(float{}, std::integral_constant<int, kMaxDimRegs>{});
 }
 
 hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
