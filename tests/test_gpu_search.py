@@ -296,3 +296,41 @@ def test_pivot_table_forms_match_oracle(u8, form, monkeypatch):
         got = g.search(Q, Q.shape[0], topk, L, n_exp=ne)
         on, od, of, oe, _ = ix.search(Q, topk, L, threads=8)
         _assert_same(got, (on, od, of), ne, oe)
+
+
+@pytest.mark.parametrize("dtype,D,M", [("uint8", 192, 48), ("uint8", 256, 64), ("float", 192, 48)])
+def test_wide_vectors_match_oracle(tmp_path, monkeypatch, dtype, D, M):
+    # dim > 128: the kernels that keep 8 rerank coordinates per lane (4-dim
+    # PQ chunks, so the unrolled ADC path); every fused form of the pivot
+    # table, the per-query LUT kernel and the beam search
+    rng = np.random.default_rng(D + M)
+    n, R = 300, 16
+    if dtype == "uint8":
+        X = rng.integers(0, 256, (n, D)).astype(np.uint8)
+        Q = rng.integers(0, 256, (40, D)).astype(np.float32)
+    else:
+        X = rng.standard_normal((n, D)).astype(np.float32)
+        Q = rng.standard_normal((40, D)).astype(np.float32)
+    adj = random_graph(rng, n, R)
+    pq = gi.train_pq(X, M, sample=n, iters=4, seed=D)
+    paths = write_custom_index(str(tmp_path), X, adj, int(rng.integers(0, n)), R, pq=pq)
+    g = _open(paths, dtype=UINT8 if dtype == "uint8" else FLOAT, nav=False)
+    ix = orc.Index(*paths[:2], "", dtype)
+    for L, topk in ((24, 10), (96, 5)):
+        on, od, of, oe, _ = ix.search(Q, topk, L)
+        runs = [(None, MODE_FUSED), (None, MODE_FUSED_LUT), (None, MODE_FUSED_GP),
+                ("half", MODE_FUSED), ("cache", MODE_FUSED)]
+        for form, mode in runs:
+            if form is None:
+                monkeypatch.delenv("GANN_PIVOT_FORM", raising=False)
+            else:
+                monkeypatch.setenv("GANN_PIVOT_FORM", form)
+            ne = np.empty(40, np.int32)
+            got = g.search(Q, 40, topk, L, n_exp=ne, mode=mode)
+            _assert_same(got, (on, od, of), ne, oe)
+        monkeypatch.delenv("GANN_PIVOT_FORM", raising=False)
+        bn, bd, bf, be = ix.search_beam(Q, topk, L, 4)
+        ne = np.empty(40, np.int32)
+        got = g.search(Q, 40, topk, L, beam_width=4, n_exp=ne)
+        _assert_same(got, (bn, bd, bf), ne, be)
+    g.close()
