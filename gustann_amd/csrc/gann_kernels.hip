@@ -442,10 +442,10 @@ struct PivotVec<2> {
 // cap a kernel at 128 VGPRs), so only the 4-slot kernels (dim <= 128) do.
 // kPivLds: piv is the whole table in LDS, at the beginning of the dynamic
 // LDS, which is LDS address 0: the kernels that call this declare no static
-// LDS, and their launchers check that with hipFuncGetAttributes.  Reading LDS rows by their address from 0 leaves the
-// row address as one 24-bit multiply of the code byte (the compiler folds the
-// byte select into it); an offset from the dynamic LDS symbol costs a second
-// VALU operation per chunk.
+// LDS, and their launchers check that with hipFuncGetAttributes.  Reading
+// LDS rows by their address from 0 leaves the row address as one 24-bit
+// multiply of the code byte (the compiler folds the byte select into it); an
+// offset from the dynamic LDS symbol costs a second VALU operation per chunk.
 template <typename PV>
 __device__ __forceinline__ PV lds_at(uint32_t a) {
   return *reinterpret_cast<const __attribute__((address_space(3))) PV*>((size_t)a);
@@ -1051,7 +1051,8 @@ void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out) {
 }
 
 namespace {
-// The shared-codebook kernels with the whole pivot table in LDS address it
+// The shared-codebook kernels address their LDS pivot tables (the whole
+// table, or the partial table of a split form with 4 rerank slots per lane)
 // from LDS address 0 (lds_at), which is where the dynamic LDS starts only
 // when the kernel has no static LDS: refuse the launch otherwise (checked for
 // every form, so that none gains static LDS unnoticed).
