@@ -411,7 +411,8 @@ void validate_search(const gann_handle* h, int32_t nq, int32_t topk, int32_t L, 
   if (nq < 0) raise(GANN_ERR_INVALID, "nq must be >= 0");
   if (topk < 1) raise(GANN_ERR_INVALID, "topk must be >= 1");
   if (L < topk) raise(GANN_ERR_INVALID, "L (ef_search) must be >= topk (bin/search_disk.cpp:189-192)");
-  if (beam < 1 || beam > gann::max_beam_width())
+  if (beam < 1) raise(GANN_ERR_INVALID, "beam_width must be >= 1 (1 = the reference's one node per iteration)");
+  if (beam > gann::max_beam_width())
     raise(GANN_ERR_UNSUPPORTED, "beam_width must be in [1, " + std::to_string(gann::max_beam_width()) +
                                     "] (1 = the reference's one node per iteration)");
   if (h->layout.max_m > 64)

@@ -93,10 +93,12 @@ class GustANN:
                 raise ValueError("output arrays must be C-contiguous int32/float32")
         if nns.size < num_queries * topk or distances.size < num_queries * topk or found_cnt.size < num_queries:
             raise ValueError("output arrays too small")
-        st = N.Stats()
-        ne = None
         if n_exp is not None:
-            ne = n_exp.ctypes.data
+            if (not isinstance(n_exp, np.ndarray) or n_exp.dtype != np.int32
+                    or not n_exp.flags.c_contiguous or n_exp.size < num_queries):
+                raise ValueError("n_exp must be a C-contiguous int32 array of at least num_queries entries")
+        st = N.Stats()
+        ne = None if n_exp is None else n_exp.ctypes.data
         N.check(N.hip_lib().gann_search_ex(self.handle, q.ctypes.data, num_queries, topk, ef_search,
                                            beam_width, mode, nns.ctypes.data, distances.ctypes.data,
                                            found_cnt.ctypes.data, ne, C.byref(st)))

@@ -127,7 +127,11 @@ int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int
 /* Asynchronous fused search on device buffers already resident in HBM,
  * enqueued on `stream` (a hipStream_t; 0 = the default stream).
  * entries_dev: [nq] device scratch for the entry ids.  n_exp_dev/n_adc_dev
- * nullable [nq]. */
+ * nullable [nq].  The kernels also use scratch owned by the handle (the
+ * query queue counter, q - centroid of every query, and the step-wise
+ * modes' LUTs, lists and states), so at most one call per handle may be in
+ * flight: a caller that enqueues calls of one handle on different streams
+ * orders them itself (or uses one handle per stream). */
 int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                        int32_t* entries_dev, int32_t* nns_dev, float* dists_dev,
                        int32_t* found_dev, int32_t* n_exp_dev, int32_t* n_adc_dev, void* stream);
