@@ -18,7 +18,8 @@ MODE_FUSED, MODE_STEPWISE, MODE_FUSED_LUT, MODE_STEPWISE_PAGED, MODE_FUSED_GP, M
 # Every symbol declared in include/gustann.h.
 ABI_SYMBOLS = (
     "gann_last_error", "gann_version", "gann_open", "gann_close", "gann_get_info",
-    "gann_search", "gann_search_ex", "gann_search_device", "gann_search_device_ex", "gann_nav_entry",
+    "gann_search", "gann_search_ex", "gann_search_device", "gann_search_device_ex",
+    "gann_search_device_noalloc", "gann_nav_entry",
     "gann_pq_open", "gann_pq_create", "gann_pq_close", "gann_handle_pq",
     "gann_pq_lut_build", "gann_pq_adc_scan", "gann_pq_adc_scan_device", "gann_knn_exact",
     "gann_diag_gather_rows", "gann_build_vamana", "gann_diag_robust_prune", "gann_pq_encode",
@@ -72,6 +73,8 @@ _SIGS = {
                                          C.POINTER(_I32)]),
     "gann_search_device_ex": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P,
                                         _P, _P]),
+    "gann_search_device_noalloc": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P,
+                                             _P, _P, _P]),
     "gann_nav_entry": (C.c_int, [_P, _P, _I32, _P, _P]),
     "gann_pq_open": (C.c_int, [C.c_char_p, _I32, C.POINTER(_P)]),
     "gann_pq_create": (C.c_int, [_P, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, C.POINTER(_P)]),

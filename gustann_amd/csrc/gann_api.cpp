@@ -267,6 +267,8 @@ struct gann_handle {
   DevBuf q, entries, local, nns, dists, found, nexp, nadc, counters, qs;
   DevBuf luts, lists, state;
   PinnedBuf counter_host;
+  // this device's copy of the fixed scratch of gann_search_device_noalloc
+  void* noalloc_scratch = nullptr;
 
   ~gann_handle() {
     if (stream) {
@@ -299,6 +301,7 @@ void open_handle(const gann_config* cfg, gann_handle* h) {
     h->lds_limit = (size_t)lds;
   }
   GANN_HIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+  GANN_HIP(gann::noalloc_scratch_setup(h->device, &h->noalloc_scratch));
   h->pq.device = h->device;
   GANN_HIP(hipStreamCreateWithFlags(&h->pq.stream, hipStreamNonBlocking));
 
@@ -750,9 +753,31 @@ void run_stepwise_paged(gann_handle* h, const float* q_dev, int32_t nq, int32_t 
   GANN_HIP(gann::launch_step_finish(nq, topk, h->state.p, nns, dists, found, nexp, nadc, s));
 }
 
-void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
-                int32_t mode, const int32_t* entries, int32_t* nns, float* dists, int32_t* found,
-                int32_t* nexp, int32_t* nadc, hipStream_t s, int32_t beam = 1) {
+// Device scratch of one search: counters (0: entry fallback count, 1:
+// step-wise active count, 2: query queue) and q - centroid of every query.
+// The handle's own buffers grow on demand; the fixed scratch of the
+// allocation-free entry point is never grown (its caller checks the size)
+// and serves the fused modes only.
+struct SearchScratch {
+  gann_handle* h;
+  int32_t* fixed_counters = nullptr;
+  float* fixed_qs = nullptr;
+  bool fixed() const { return fixed_counters != nullptr; }
+  int32_t* counters() {
+    if (fixed()) return fixed_counters;
+    h->counters.ensure(64);
+    return h->counters.as<int32_t>();
+  }
+  float* qs(int64_t nfloats) {
+    if (fixed()) return fixed_qs;
+    h->qs.ensure((size_t)nfloats * 4);
+    return h->qs.as<float>();
+  }
+};
+
+void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t nq, int32_t topk,
+                int32_t L, int32_t mode, const int32_t* entries, int32_t* nns, float* dists,
+                int32_t* found, int32_t* nexp, int32_t* nadc, hipStream_t s, int32_t beam = 1) {
   const gann::DiskLayout& Ly = h->layout;
   // Shared-codebook kernels: one workgroup per CU holding the pivot table and
   // as many lists as fit; below kMinLdsWaves lists, the pivots are read
@@ -767,12 +792,11 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
     const bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
     const int waves = gp ? w_gp : w_lds;
     if (waves < 1) raise(GANN_ERR_UNSUPPORTED, "beam_width > 1 needs one list in LDS");
-    h->counters.ensure(64);
-    h->qs.ensure((size_t)nq * Ly.dim * 4);
+    int32_t* ctr = sc.counters();
+    float* qs = sc.qs((int64_t)nq * Ly.dim);
     const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
     GANN_HIP(gann::launch_search_beam(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, beam,
-                                      nns, dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
-                                      h->qs.as<float>(), waves, blocks, gp, s));
+                                      nns, dists, found, nexp, nadc, ctr + 2, qs, waves, blocks, gp, s));
     return;
   }
   if (mode == GANN_MODE_FUSED || mode == GANN_MODE_FUSED_GP) {
@@ -810,12 +834,12 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
     }
     const int waves = gp ? gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true, g, chunk_w) : w_lds;
     if (waves >= 1 && (gp || waves >= 2)) {
-      h->counters.ensure(64);
-      h->qs.ensure((size_t)nq * Ly.dim * 4);
+      int32_t* ctr = sc.counters();
+      float* qs = sc.qs((int64_t)nq * Ly.dim);
       const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
       GANN_HIP(gann::launch_search_cb(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,
-                                      dists, found, nexp, nadc, h->counters.as<int32_t>() + 2,
-                                      h->qs.as<float>(), waves, blocks, gp, gp ? g : 0, s));
+                                      dists, found, nexp, nadc, ctr + 2, qs, waves, blocks, gp,
+                                      gp ? g : 0, s));
       return;
     }
     if (mode == GANN_MODE_FUSED_GP)
@@ -829,6 +853,9 @@ void run_search(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, in
                                  dists, found, nexp, nadc, s));
     return;
   }
+  if (sc.fixed())
+    raise(GANN_ERR_UNSUPPORTED, "the step-wise modes keep per-query LUTs and lists in scratch "
+                                "allocated by the handle: use gann_search_device_ex for them");
   if (mode == GANN_MODE_STEPWISE_PAGED || mode == GANN_MODE_STEPWISE_URING) {
     run_stepwise_paged(h, q_dev, nq, topk, L, entries, nns, dists, found, nexp, nadc, s,
                        mode == GANN_MODE_STEPWISE_URING);
@@ -941,9 +968,10 @@ int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int
     run_entries(h, h->q.as<float>(), nq, h->entries.as<int32_t>(), nullptr, h->counters.as<int32_t>(), s);
     GANN_HIP(hipStreamSynchronize(s));
     const double t1 = now_s();
-    run_search(h, h->q.as<float>(), nq, topk, L, mode, h->entries.as<int32_t>(), h->nns.as<int32_t>(),
-               h->dists.as<float>(), h->found.as<int32_t>(), h->nexp.as<int32_t>(),
-               h->nadc.as<int32_t>(), s, beam_width);
+    SearchScratch sc{h};
+    run_search(h, sc, h->q.as<float>(), nq, topk, L, mode, h->entries.as<int32_t>(),
+               h->nns.as<int32_t>(), h->dists.as<float>(), h->found.as<int32_t>(),
+               h->nexp.as<int32_t>(), h->nadc.as<int32_t>(), s, beam_width);
     GANN_HIP(hipStreamSynchronize(s));
     const double t2 = now_s();
     GANN_HIP(hipMemcpyAsync(nns, h->nns.p, (size_t)nq * topk * 4, hipMemcpyDeviceToHost, s));
@@ -993,9 +1021,40 @@ int gann_search_device_ex(gann_handle* h, const float* q_dev, int32_t nq, int32_
       raise(GANN_ERR_INVALID, "NULL buffer");
     GANN_HIP(hipSetDevice(h->device));
     hipStream_t s = (hipStream_t)stream;
-    h->counters.ensure(64);
-    run_entries(h, q_dev, nq, entries_dev, nullptr, h->counters.as<int32_t>(), s);
-    run_search(h, q_dev, nq, topk, L, mode, entries_dev, nns_dev, dists_dev, found_dev, n_exp_dev,
+    SearchScratch sc{h};
+    run_entries(h, q_dev, nq, entries_dev, nullptr, sc.counters(), s);
+    run_search(h, sc, q_dev, nq, topk, L, mode, entries_dev, nns_dev, dists_dev, found_dev, n_exp_dev,
+               n_adc_dev, s, beam_width);
+  });
+}
+
+int gann_search_device_noalloc(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                               int32_t beam_width, int32_t mode, int32_t* entries_dev, int32_t* nns_dev,
+                               float* dists_dev, int32_t* found_dev, int32_t* n_exp_dev,
+                               int32_t* n_adc_dev, void* stream) {
+  return guarded([&] {
+    if (!h) raise(GANN_ERR_INVALID, "handle is NULL");
+    validate_search(h, nq, topk, L, beam_width);
+    if (mode != GANN_MODE_FUSED && mode != GANN_MODE_FUSED_GP && mode != GANN_MODE_FUSED_LUT)
+      raise(GANN_ERR_UNSUPPORTED, "gann_search_device_noalloc runs the fused modes only "
+                                  "(GANN_MODE_FUSED, GANN_MODE_FUSED_GP, GANN_MODE_FUSED_LUT)");
+    const int64_t qs_bytes = (int64_t)nq * h->layout.dim * 4;
+    const int64_t cap = (int64_t)(gann::kNoAllocScratchBytes - gann::kNoAllocCounterBytes);
+    if (qs_bytes > cap)
+      raise(GANN_ERR_INVALID, "gann_search_device_noalloc: nq * dim * 4 = " + std::to_string(qs_bytes) +
+                                  " bytes exceeds its fixed scratch of " + std::to_string(cap) +
+                                  " bytes (at most " + std::to_string(cap / (h->layout.dim * 4)) +
+                                  " queries of this index per call)");
+    if (nq == 0) return;
+    if (!q_dev || !entries_dev || !nns_dev || !dists_dev || !found_dev)
+      raise(GANN_ERR_INVALID, "NULL buffer");
+    if (!h->noalloc_scratch) raise(GANN_ERR_HIP, "fixed scratch was not resolved for this device");
+    GANN_HIP(hipSetDevice(h->device));
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t* base = (uint8_t*)h->noalloc_scratch;
+    SearchScratch sc{h, (int32_t*)base, (float*)(base + gann::kNoAllocCounterBytes)};
+    run_entries(h, q_dev, nq, entries_dev, nullptr, sc.counters(), s);
+    run_search(h, sc, q_dev, nq, topk, L, mode, entries_dev, nns_dev, dists_dev, found_dev, n_exp_dev,
                n_adc_dev, s, beam_width);
   });
 }

@@ -19,7 +19,9 @@
 
 #include <climits>
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "gann_device.hpp"
 #include "gann_list.hpp"
@@ -1242,6 +1244,36 @@ hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream)
   hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
                      n, v);
   return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ fixed scratch
+
+// Scratch of the allocation-free search entry point: its counters (entry
+// fallback count, query queue) and q - centroid of every query.  Each GPU
+// that loads this library holds its own copy until the process ends.  In
+// host code the name `scratch` is not a device address: the copy of the
+// current device is resolved below with hipGetSymbolAddress, and only that
+// pointer is handed to kernels and fills.
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_dev;  // per device id
+}  // namespace
+
+hipError_t noalloc_scratch_setup(int device, void** out) {
+  if (device < 0 || !out) return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if ((size_t)device >= g_scratch_dev.size()) g_scratch_dev.resize((size_t)device + 1, nullptr);
+  if (!g_scratch_dev[(size_t)device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_dev[(size_t)device] = p;
+  }
+  *out = g_scratch_dev[(size_t)device];
+  return hipSuccess;
 }
 
 }  // namespace gann

@@ -64,4 +64,14 @@ hipError_t launch_step_finish(int nq, int topk, const void* st, int32_t* nns, fl
                               int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
 
+// Fixed device scratch of the allocation-free search entry point
+// (gann_search_device_noalloc): kNoAllocCounterBytes of counters, then
+// q - centroid of every query from byte kNoAllocCounterBytes on.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+constexpr size_t kNoAllocCounterBytes = 256;
+// The device address of the current device's copy of that scratch, resolved
+// once per device (hipGetSymbolAddress) and cached; call with `device`
+// current.
+hipError_t noalloc_scratch_setup(int device, void** out);
+
 }  // namespace gann

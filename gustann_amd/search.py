@@ -128,6 +128,16 @@ class GustANN:
                                                   entries_ptr, nns_ptr, dists_ptr, found_ptr,
                                                   nexp_ptr, nadc_ptr, stream))
 
+    def search_device_noalloc(self, q_ptr, nq, topk, L, entries_ptr, nns_ptr, dists_ptr, found_ptr,
+                              nexp_ptr=None, nadc_ptr=None, stream=None, beam_width=1,
+                              mode=N.MODE_FUSED):
+        """search_device with the kernels' scratch in the library's fixed
+        device array: no device allocation (fused modes; nq * dim * 4 bytes
+        at most 64 MiB - 256 B; calls that overlap on one GPU race)."""
+        N.check(N.hip_lib().gann_search_device_noalloc(self.handle, q_ptr, nq, topk, L, beam_width, mode,
+                                                       entries_ptr, nns_ptr, dists_ptr, found_ptr,
+                                                       nexp_ptr, nadc_ptr, stream))
+
     def pq(self) -> "PQSearch":
         p = C.c_void_p()
         N.check(N.hip_lib().gann_handle_pq(self.handle, C.byref(p)))

@@ -144,6 +144,22 @@ int gann_search_device_ex(gann_handle* h, const float* q_dev, int32_t nq, int32_
                           float* dists_dev, int32_t* found_dev, int32_t* n_exp_dev,
                           int32_t* n_adc_dev, void* stream);
 
+/* gann_search_device_ex without any allocation, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * kernels' scratch (counters and q - centroid of every query) lives in a
+ * fixed device array of 64 MiB that each GPU holds until the process ends,
+ * so nq * dim * 4 must not exceed 64 MiB - 256 B (131071 queries at dim
+ * 128); larger calls return GANN_ERR_INVALID.  Fused modes only
+ * (GANN_MODE_FUSED, GANN_MODE_FUSED_GP, GANN_MODE_FUSED_LUT; the step-wise
+ * modes return GANN_ERR_UNSUPPORTED).  Every call on one GPU shares that
+ * array, whichever handle it comes from: calls that overlap on one GPU race,
+ * so the caller orders them.  Arguments and results as gann_search_device_ex. */
+int gann_search_device_noalloc(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
+                               int32_t beam_width, int32_t mode, int32_t* entries_dev, int32_t* nns_dev,
+                               float* dists_dev, int32_t* found_dev, int32_t* n_exp_dev,
+                               int32_t* n_adc_dev, void* stream);
+
 /* get_entry_kernel + NavGraph::translate: base-graph entry per query (the
  * medoid when the handle has no pivot graph).  local_out (nullable) receives
  * the pivot-local ids. */
