@@ -1,22 +1,40 @@
 #!/usr/bin/env python3
-"""Benchmark of the GustANN MI355X search path.
+"""Benchmark of the GustANN MI355X in-memory search path.
 
-Default workload (the PQ kernel microbenchmark): 10,000 f32 queries of dim
-128, PQ with M = 32 subspaces x 256 centroids, 100,000,000 random 32-byte code
-rows resident in HBM, 4096 uniformly random candidate ids per query.  One
-step = one launch of the fused LUT-build + ADC gather-scan kernel over all
-queries.  Prints one JSON line:
+Default workload, the headline "QPS @ recall@10=0.9" on one MI355X: the
+100M x 128 uint8 index --
+  * 100,000,000 points of a seeded Gaussian mixture (10,000 centres uniform
+    in [32, 224]^128, sigma 12, rounded and clipped), 10,000 queries from the
+    same mixture;
+  * Vamana graph R=64, L_build=100, alpha=1.2 (the GPU builder), a
+    1,000,000-node pivot graph (R=32, L=50), PQ M=32 x 256;
+  * pages, codes and pivot graph resident in HBM (about 45 GB);
+  * exact top-10 ground truth for all 10,000 queries;
+built in this run (nothing persists between runs; a --data-dir whose
+meta.json holds the same spec is reused).  The smallest L whose recall@10
+over all queries reaches 0.9 is found by a coarse sweep and a step-16 scan;
+then one step = one pass of the search path (entry selection on the pivot
+graph + the fused beam search) over the 10,000 queries, inputs resident in
+HBM, timed with HIP events on the launch stream.  One JSON line:
 
-  value      queries/s of the kernel (inputs already resident in HBM)
-  roofline   algorithmic bytes per launch / average launch time vs 8 TB/s
-  cpu_baseline  the CPU oracle on a bounded sample of the same workload
+  value         queries/s at that L (whole job, one GPU)
+  roofline      the fused search kernel alone: algorithmic bytes per launch
+                (per expansion the record and the neighbours' code rows, per
+                query the query and its results) / its average launch time
+  cpu_baseline  the CPU oracle (the same algorithm in C) at that L on every
+                core the process may use, one pinned thread per core, on a
+                bounded sample of the queries
+  adc_microbench  the PQ kernel microbenchmark (LUT build + ADC gather-scan
+                over 100M random 32-byte code rows) with its own roofline
 
-``--workload search`` runs the in-memory beam search on a synthetic
-uint8 mixture index instead (built on the fly; slower to set up).
+Other workloads: --workload search (any synthetic index), adc, knn, gather,
+copy (diagnostics).
 """
 from __future__ import annotations
 
 import argparse
+import dataclasses
+import hashlib
 import json
 import os
 import sys
@@ -29,11 +47,348 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "QPS @ recall@10=0.9 on 1 MI355X; ADC-scan HBM GB/s vs peak"
+RECALL_TARGET = 0.9
+COARSE_L = (1024, 1536, 2048, 2304, 2560, 2816, 3072, 3584, 4096, 5120, 6144, 8192)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
+
+# ------------------------------------------------------------------ helpers
+
+def recall_at_k(res, gt, k):
+    """calc_recall (bin/utils.hpp:104-116): hits of each result slot in the
+    set of the first k ground-truth ids, over the ground-truth rows (a
+    duplicated id counts once per occurrence)."""
+    n = gt.shape[0]
+    r = np.asarray(res[:n, :k])
+    g = np.asarray(gt[:n, :k])
+    return float((r[:, :, None] == g[:, None, :]).any(-1).sum()) / (n * k)
+
+
+def profile_json(name):
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_info():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    return orc.cpu_cores()
+
+
+def c3_spec():
+    from gustann_amd import index as gi
+    return gi.DatasetSpec(name="c3_100m_u8", n=100_000_000, dim=128, dtype="uint8", nclusters=10_000,
+                          sigma=12.0, R=64, L_build=100, alpha=1.2, M=32, nq=10_000, k=10,
+                          nav_n=1_000_000, nav_R=32, nav_L=50, gt_nq=0, builder="gpu")
+
+
+def dataset(spec, data_dir=""):
+    """The dataset of `spec`: reused from data_dir (or the default directory
+    named by a hash of the whole spec) when its meta.json holds exactly this
+    spec, else built there."""
+    from gustann_amd import index as gi
+    sd = dataclasses.asdict(spec)
+    key = hashlib.sha1(json.dumps(sd, sort_keys=True).encode()).hexdigest()[:12]
+    out_dir = data_dir or os.path.join("/tmp", f"gann_{spec.name}_{key}")
+    meta_path = os.path.join(out_dir, "meta.json")
+    if os.path.exists(meta_path):
+        with open(meta_path) as f:
+            meta = json.load(f)
+        if meta.get("spec") == json.loads(json.dumps(sd)):
+            log(f"[bench] reusing {out_dir}")
+            return meta
+        log(f"[bench] {out_dir} holds another spec: rebuilding")
+    log(f"[bench] building {spec.name} under {out_dir}")
+    return gi.build_dataset(spec, out_dir, verbose=True)
+
+
+class DeviceSearch:
+    """One open handle plus device buffers for nq queries; every launch goes
+    through gann_search_device_ex on the torch stream."""
+
+    def __init__(self, meta, Q, topk, placement="hbm"):
+        import torch
+        from gustann_amd.search import FLOAT, GustANN, GustANNConfig, UINT8
+        P = meta["paths"]
+        u8 = meta["spec"]["dtype"] == "uint8"
+        self.g = GustANN(UINT8 if u8 else FLOAT)
+        t = time.perf_counter()
+        self.g.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), placement == "hbm")
+        log(f"[bench] index open ({placement}) {time.perf_counter() - t:.1f} s")
+        self.torch = torch
+        dev = torch.device("cuda:0")
+        self.nq, self.k = Q.shape[0], topk
+        self.q = torch.from_numpy(np.ascontiguousarray(Q, np.float32)).to(dev)
+        self.ent = torch.empty(self.nq, dtype=torch.int32, device=dev)
+        self.nns = torch.empty((self.nq, topk), dtype=torch.int32, device=dev)
+        self.dd = torch.empty((self.nq, topk), dtype=torch.float32, device=dev)
+        self.fc = torch.empty(self.nq, dtype=torch.int32, device=dev)
+        self.ne = torch.empty(self.nq, dtype=torch.int32, device=dev)
+        self.na = torch.empty(self.nq, dtype=torch.int32, device=dev)
+        self.stream = torch.cuda.current_stream(dev)
+        self.dim = int(self.g.info.dim)
+        self.M = int(self.g.info.num_chunks)
+        self.elem = 1 if u8 else 4
+
+    def launch(self, L, beam=1, mode=0, entries_given=False):
+        from gustann_amd import _native as N
+        m = mode | (N.SEARCH_ENTRIES_GIVEN if entries_given else 0)
+        self.g.search_device(self.q.data_ptr(), self.nq, self.k, L, self.ent.data_ptr(), self.nns.data_ptr(),
+                             self.dd.data_ptr(), self.fc.data_ptr(), self.ne.data_ptr(), self.na.data_ptr(),
+                             self.stream.cuda_stream, beam_width=beam, mode=m)
+
+    def timed(self, L, steps, warmup, **kw):
+        """Average ms per launch over `steps` launches after `warmup`,
+        bracketed by device synchronisations, from HIP events recorded on
+        the stream the kernels run on."""
+        torch = self.torch
+        for _ in range(warmup):
+            self.launch(L, **kw)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t = time.perf_counter()
+        e0.record(self.stream)
+        for _ in range(steps):
+            self.launch(L, **kw)
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps, time.perf_counter() - t
+
+    def results(self):
+        return self.nns.cpu().numpy(), self.dd.cpu().numpy(), self.fc.cpu().numpy()
+
+    def alg_bytes(self):
+        """Algorithmic bytes of the last launch: per expansion the record
+        read (coordinates + degree + neighbour ids), per ADC the code row
+        and the neighbour id, per query the query vector and its results."""
+        exps = int(self.ne.sum().item())
+        adcs = int(self.na.sum().item())
+        return (exps * (self.dim * self.elem + 4) + adcs * (4 + self.M)
+                + self.nq * (4 * self.dim + 8 * self.k)), exps, adcs
+
+    def close(self):
+        self.g.close()
+
+
+def find_L(ds, gt, k, beam=1, mode=0, coarse=COARSE_L, step=16):
+    """Smallest swept L with recall@10 >= 0.9: the coarse list until one
+    reaches it, then every `step` above the last coarse L that did not.
+    Returns (L or None, sweep rows)."""
+    rows = []
+
+    def rec(L):
+        ds.launch(L, beam=beam, mode=mode)
+        ds.torch.cuda.synchronize()
+        nns = ds.nns.cpu().numpy()
+        r = recall_at_k(nns, gt, 10)
+        rows.append({"L": L, "recall_at_10": r})
+        log(f"[bench] sweep L={L} recall@10={r:.4f}")
+        return r
+
+    prev = None
+    hit = None
+    for L in coarse:
+        if L < k:
+            continue
+        if rec(L) >= RECALL_TARGET:
+            hit = L
+            break
+        prev = L
+    if hit is None:
+        return None, rows
+    if prev is not None:
+        for L in range(prev + step, hit, step):
+            if rec(L) >= RECALL_TARGET:
+                return L, rows
+    return hit, rows
+
+
+def cpu_baseline_search(meta, Q, topk, L, beam, target_s):
+    """The oracle's search (orc_search, or orc_search_beam for beam > 1) at L
+    on every CPU the process may use, one pinned thread per core, over the
+    first queries that take about target_s.  Returns (record, (nns, dists,
+    found) of the sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    P = meta["paths"]
+    t = time.perf_counter()
+    ix = orc.Index(P["index"], P["pq"], P["nav"], dtype=meta["spec"]["dtype"])
+    log(f"[bench] oracle index load {time.perf_counter() - t:.1f} s")
+    cores, model = orc.cpu_cores()
+    orc.set_pin_threads(True)
+
+    def run(Qs):
+        if beam > 1:
+            return ix.search_beam(Qs, topk, L, beam, threads=cores)[:3]
+        return ix.search(Qs, topk, L, threads=cores)[:3]
+
+    n0 = min(Q.shape[0], 2 * cores)
+    t = time.perf_counter()
+    run(Q[:n0])
+    per_q = (time.perf_counter() - t) / n0
+    n = int(min(Q.shape[0], max(n0, target_s / max(per_q, 1e-9))))
+    t = time.perf_counter()
+    out = run(Q[:n])
+    dt = time.perf_counter() - t
+    orc.set_pin_threads(False)
+    rec = {"value": n / dt, "unit": "queries/s", "cores": cores, "kind": "port",
+           "sample": (f"first {n} of {Q.shape[0]} queries at L={L}, top-{topk}: oracle/gann_oracle.c "
+                      f"{'orc_search_beam (beam ' + str(beam) + ')' if beam > 1 else 'orc_search'}, "
+                      f"{cores} threads pinned one per core, {dt:.1f} s; CPU: {model}")}
+    return rec, out
+
+
+# ------------------------------------------------------------------ headline
+
+def bench_c3(args):
+    import torch
+    from gustann_amd import index as gi
+    spec = c3_spec()
+    t0 = time.perf_counter()
+    meta = dataset(spec, args.data_dir)
+    build_s = time.perf_counter() - t0
+    P = meta["paths"]
+    Q = gi.read_vecs(P["query"], np.uint8).astype(np.float32)
+    gt = gi.read_vecs(P["gt"], np.int32)
+    K = 10
+    ds = DeviceSearch(meta, Q, K)
+    if args.L:
+        L, sweep = args.L[0], []
+    else:
+        L, sweep = find_L(ds, gt, K)
+        if L is None:
+            print(json.dumps({"metric": METRIC, "value": None, "error":
+                              f"recall@10 stays below {RECALL_TARGET} up to L={COARSE_L[-1]}",
+                              "sweep": sweep}), flush=True)
+            sys.exit(1)
+    log(f"[bench] L={L}: {args.warmup} warmup + {args.steps} timed steps")
+    ms, wall = ds.timed(L, args.steps, args.warmup)
+    nns, dd, fc = ds.results()
+    rec10 = recall_at_k(nns, gt, 10)
+    # the fused search kernel alone (entries given): roofline
+    ms_k, _ = ds.timed(L, args.steps, 1, entries_given=True)
+    alg, exps, adcs = ds.alg_bytes()
+    achieved = alg / (ms_k / 1e3) / 1e9
+    value = ds.nq / (ms / 1e3)
+    log(f"[bench] L={L}: {ms:.3f} ms/step ({value:.0f} QPS, recall@10 {rec10:.4f}); search kernel "
+        f"{ms_k:.3f} ms, {achieved:.1f} GB/s algorithmic; {exps / ds.nq:.1f} expansions/query")
+    prof = profile_json("search_cb_c3_traffic.json")
+    traffic = prof.get("traffic_bytes_per_launch") if prof and prof.get("L") == L else None
+    result = {
+        "metric": METRIC, "value": value, "unit": "queries/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": ("synthetic: seeded uint8 Gaussian mixture (10k centres in [32,224]^128, sigma 12), "
+                 "index built in this run"),
+        "config": {"workload": "100M x 128 uint8 index (Vamana R=64 L=100 alpha=1.2, 1M-node pivot graph, "
+                               "PQ M=32 x 256, all in HBM), 10k queries, top-10, L at recall@10 >= 0.9",
+                   "num_pts": spec.n, "dim": spec.dim, "R": spec.R, "M": spec.M, "nq": ds.nq, "topk": K,
+                   "L": L, "recall_at_10": rec10, "recall_queries": int(gt.shape[0]),
+                   "expansions_per_query": exps / ds.nq, "L_sweep": sweep,
+                   "search_kernel_ms": ms_k, "entry_selection_ms": ms - ms_k,
+                   "dataset_build_s": meta.get("build_s") if build_s > 60 else None,
+                   "dataset_ready_s": build_s, "timed_wall_s": wall},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "alg_bytes_per_launch": alg,
+                     "kernel": "search_cb_kernel (fused beam search, pivot table through the caches)"},
+    }
+    if not args.no_cpu:
+        log(f"[bench] CPU baseline (oracle) at L={L}")
+        cpu, (on, od, of) = cpu_baseline_search(meta, Q, K, L, 1, args.cpu_seconds)
+        result["cpu_baseline"] = cpu
+        n = on.shape[0]
+        result["parity_sample_bitexact"] = bool(np.array_equal(nns[:n], on) and np.array_equal(fc[:n], of)
+                                                and np.array_equal(dd[:n].view(np.uint32), od.view(np.uint32)))
+    ds.close()
+    del ds
+    torch.cuda.empty_cache()
+    if not args.no_adc:
+        a = argparse.Namespace(**vars(args))
+        a.cpu_seconds = args.adc_cpu_seconds
+        result["adc_microbench"] = bench_adc(a, nested=True)
+    return result
+
+
+# ------------------------------------------------------------------ generic search
+
+def bench_search(args):
+    from gustann_amd import index as gi
+    u8 = args.dtype == "uint8"
+    sigma = args.sigma if args.sigma > 0 else (12.0 if u8 else 0.05)
+    K = args.topk
+    spec = gi.DatasetSpec(name=f"mix{args.n}x{args.dim}{'' if u8 else 'f'}"
+                               + (f"z{args.zipf}" if args.zipf > 0 else ""),
+                          n=args.n, dim=args.dim, dtype=args.dtype, nclusters=args.nclusters,
+                          sigma=sigma, R=args.R, L_build=100, M=args.M, nq=args.nq_search,
+                          k=max(10, K), nav_n=args.nav_n, gt_nq=args.gt_nq, zipf_s=args.zipf,
+                          builder=args.builder,
+                          extra_queries=[{"name": a, "nq": int(b), "zipf_s": float(c), "k": int(d),
+                                          "gt_nq": args.gt_nq}
+                                         for a, b, c, d in (x.split(":") for x in args.extra_query_set)])
+    meta = dataset(spec, args.data_dir)
+    P = meta["paths"]
+    qk = f"query_{args.query_set}" if args.query_set else "query"
+    if qk not in P:
+        raise SystemExit(f"query set {args.query_set!r} was not built with this index")
+    Q = gi.read_vecs(P[qk], np.uint8 if u8 else np.float32).astype(np.float32)
+    gt = gi.read_vecs(P[f"gt_{args.query_set}" if args.query_set else "gt"], np.int32)
+    Qr = np.tile(Q, (args.repeat, 1))
+    ds = DeviceSearch(meta, Qr, K, args.placement)
+    mode = {"fused": 0, "stepwise": 1, "lut": 2, "paged": 3, "gp": 4, "uring": 5}[args.mode]
+    rows = []
+    for L in sorted(args.L):
+        ms, _ = ds.timed(L, args.steps, args.warmup, beam=args.beam, mode=mode)
+        nns, _, _ = ds.results()
+        alg, exps, adcs = ds.alg_bytes()
+        rec = recall_at_k(nns, gt, K)
+        rec10 = recall_at_k(nns, gt, 10)
+        rows.append({"L": L, "ms": ms, "qps": ds.nq / (ms / 1e3), "recall": rec, "recall_at_10": rec10,
+                     "expansions_per_query": exps / ds.nq, "alg_GBps": alg / (ms / 1e3) / 1e9})
+        log(f"[bench] L={L} {ms:.3f} ms qps={ds.nq / (ms / 1e3):.0f} recall@{K}={rec:.4f} recall@10={rec10:.4f}")
+    best = next((r for r in rows if r["recall_at_10"] >= RECALL_TARGET), None)
+    result = {
+        "metric": METRIC, "value": best["qps"] if best else None, "unit": "queries/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": best["ms"] if best else None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": ("synthetic uint8 Gaussian mixture" if u8 else
+                 f"synthetic L2-normalised f32 Gaussian mixture (sigma {sigma})"),
+        "config": {"workload": (f"in_memory_search_{args.n}x{args.dim}_{'u8' if u8 else 'f32'}_R{args.R}_M{args.M}"
+                                + ("" if args.placement == "hbm" else "_host_pinned")
+                                + ("" if args.mode == "fused" else f"_{args.mode}")
+                                + ("" if args.beam == 1 else f"_beam{args.beam}")
+                                + ("" if K == 10 else f"_top{K}")
+                                + ("" if args.zipf <= 0 else f"_zipf{args.zipf}")
+                                + ("" if not args.query_set else f"_queries_{args.query_set}")),
+                   "nq": ds.nq, "L": best["L"] if best else None, "L_sweep": rows,
+                   "recall_queries": int(gt.shape[0]), "index_builder": args.builder,
+                   "index_build_s": meta.get("build_s")},
+    }
+    if best:
+        result["roofline"] = {"bound": "hbm", "achieved": best["alg_GBps"], "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": best["alg_GBps"] / HBM_PEAK_GBS, "traffic": None}
+    pick = best or rows[-1]
+    if not args.no_cpu:
+        ds.timed(pick["L"], 1, 0, beam=args.beam, mode=mode)
+        nns, dd, fc = ds.results()
+        cpu, (on, od, of) = cpu_baseline_search(meta, Q, K, pick["L"], args.beam, args.cpu_seconds)
+        result["cpu_baseline"] = cpu
+        n = on.shape[0]
+        result["parity_sample_bitexact"] = bool(np.array_equal(nns[:n], on) and np.array_equal(fc[:n], of)
+                                                and np.array_equal(dd[:n].view(np.uint32), od.view(np.uint32)))
+    ds.close()
+    return result
+
+
+# ------------------------------------------------------------------ PQ microbenchmark
 
 def adc_alg_bytes(nq, dim, S, M):
     """Algorithmic bytes of one ADC launch: per query the query vector (4*dim),
@@ -45,53 +400,34 @@ def adc_alg_bytes(nq, dim, S, M):
 def cpu_baseline_adc(pq_np, codes_host, Q, ids_host, target_s):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
-    threads = min(16, os.cpu_count() or 1)
+    cores, model = orc.cpu_cores()
+    orc.set_pin_threads(True)
     piv, cen, off = pq_np
-    # calibrate on a small batch, then run about target_s of work: a prefix
-    # of the queries, or whole passes over all of them when one pass is short
     n0 = min(64, Q.shape[0])
     t = time.perf_counter()
-    orc.adc_scan(piv, cen, off, codes_host, Q[:n0], ids_host[:n0], threads)
+    orc.adc_scan(piv, cen, off, codes_host, Q[:n0], ids_host[:n0], cores)
     per_q = (time.perf_counter() - t) / n0
     n = int(min(Q.shape[0], max(n0, target_s / max(per_q, 1e-9))))
-    # the calibration batch runs cold, so keep adding whole passes until the
-    # timed work reaches target_s (a prefix shorter than all queries runs once)
     passes = 0
     t = time.perf_counter()
     while True:
-        out = orc.adc_scan(piv, cen, off, codes_host, Q[:n], ids_host[:n], threads)
+        out = orc.adc_scan(piv, cen, off, codes_host, Q[:n], ids_host[:n], cores)
         passes += 1
         dt = time.perf_counter() - t
         if n < Q.shape[0] or dt >= target_s:
             break
-    return {"value": passes * n / dt, "unit": "queries/s", "cores": threads, "kind": "port",
+    orc.set_pin_threads(False)
+    return {"value": passes * n / dt, "unit": "queries/s", "cores": cores, "kind": "port",
             "sample": f"{passes} pass(es) over the first {n} of the {Q.shape[0]} queries x "
                       f"{ids_host.shape[1]} ids: oracle/gann_oracle.c orc_adc_scan over the full "
-                      f"host copy of the codes, {threads} threads, {dt:.1f} s"}, out
+                      f"host copy of the codes, {cores} threads pinned one per core, {dt:.1f} s; "
+                      f"CPU: {model}"}, out
 
 
-def recall_at_k(res, gt, k):
-    """calc_recall (bin/utils.hpp:104-116): hits of each result slot in the set
-    of the first k ground-truth ids, over the ground-truth rows."""
-    hits = 0
-    for r, g in zip(res, gt):
-        s = set(int(x) for x in g[:k])
-        hits += sum(1 for x in r[:k] if int(x) in s)
-    return hits / (gt.shape[0] * k)
-
-
-def traffic_from_profiles(name):
-    path = os.path.join(ROOT, "profiles", name)
-    if not os.path.exists(path):
-        return None
-    try:
-        with open(path) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
-    except Exception:
-        return None
-
-
-def bench_adc(args):
+def bench_adc(args, nested=False):
+    """PQ kernel microbenchmark: 10k f32 queries of dim 128, PQ M=32 x 256,
+    100M uniformly random 32-byte code rows in HBM, 4096 random ids per
+    query; one step = one launch of the LUT-build + ADC gather-scan kernel."""
     import torch
     from gustann_amd.search import PQSearch
 
@@ -104,7 +440,7 @@ def bench_adc(args):
     off = np.arange(0, dim + 1, dim // M, dtype=np.int32)
     g = torch.Generator(device=dev)
     g.manual_seed(7)
-    log(f"[bench] generating {N} x {M} codes and {nq} x {S} ids on the device")
+    log(f"[bench] ADC microbenchmark: {N} x {M} codes and {nq} x {S} ids generated on the device")
     codes = torch.randint(0, 256, (N, M), dtype=torch.uint8, device=dev, generator=g)
     ids = torch.randint(0, N, (nq, S), dtype=torch.int32, device=dev, generator=g)
     q_dev = torch.from_numpy(Q).to(dev)
@@ -129,26 +465,26 @@ def bench_adc(args):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
-    value = nq / (ms / 1e3)
     alg = adc_alg_bytes(nq, dim, S, M)
     achieved = alg / (ms / 1e3) / 1e9
-    log(f"[bench] {args.steps} steps: {ms:.4f} ms/step (events), wall {wall:.3f} s, "
-        f"{achieved:.1f} GB/s algorithmic")
-
+    log(f"[bench] ADC: {args.steps} steps, {ms:.4f} ms/step, {achieved:.1f} GB/s algorithmic")
+    prof = profile_json("adc_scan_c1_traffic.json")
     result = {
-        "metric": METRIC, "value": value, "unit": "queries/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (uniform random codes, ids and queries, seeded)",
+        "metric": "PQ LUT build + ADC gather-scan: queries/s (4096 candidates each)", "value": nq / (ms / 1e3),
+        "unit": "queries/s", "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "dtype": "f32", "data": "synthetic (uniform random codes, ids and queries, seeded)",
         "config": {"workload": "pq_adc_microbench", "nq": nq, "dim": dim, "M": M, "K": 256,
-                   "num_codes": N, "ids_per_query": S},
+                   "num_codes": N, "ids_per_query": S, "timed_wall_s": wall},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_from_profiles("adc_scan_c1_traffic.json"),
-                     "alg_bytes_per_launch": alg},
+                     "traffic": prof.get("traffic_bytes_per_launch") if prof else None,
+                     "alg_bytes_per_launch": alg, "kernel": "pq_adc_scan_kernel"},
     }
-    if not args.no_cpu:
-        log("[bench] CPU baseline (oracle) on a bounded sample")
+    if not nested:
+        result.update({"metric": METRIC, "n_gpus": 1, "higher_is_better": True, "scaling": "weak",
+                       "vs_baseline": None})
+    if not args.no_cpu and args.cpu_seconds > 0:
+        log("[bench] ADC CPU baseline (oracle) on a bounded sample")
         codes_host = codes.cpu().numpy()
         ids_host = ids.cpu().numpy()
         cpu, cpu_out = cpu_baseline_adc((piv, cen, off), codes_host, Q, ids_host, args.cpu_seconds)
@@ -157,129 +493,12 @@ def bench_adc(args):
         result["parity_sample_bitexact"] = bool(np.array_equal(gpu_out.view(np.uint32),
                                                                cpu_out.view(np.uint32)))
     pq.close()
+    del codes, ids, out
+    torch.cuda.empty_cache()
     return result
 
 
-def bench_search(args):
-    import torch
-    from gustann_amd import index as gi
-    from gustann_amd.search import FLOAT, GustANN, GustANNConfig, UINT8
-
-    u8 = args.dtype == "uint8"
-    sigma = args.sigma if args.sigma > 0 else (12.0 if u8 else 0.05)
-    K = args.topk
-    spec = gi.DatasetSpec(name=f"mix{args.n}x{args.dim}{'' if u8 else 'f'}"
-                               + (f"z{args.zipf}" if args.zipf > 0 else ""),
-                          n=args.n, dim=args.dim, dtype=args.dtype, nclusters=args.nclusters,
-                          sigma=sigma, R=64, L_build=100, M=args.M, nq=args.nq_search,
-                          k=max(10, K), nav_n=args.nav_n, gt_nq=args.gt_nq, zipf_s=args.zipf,
-                          builder=args.builder,
-                          extra_queries=[{"name": a, "nq": int(b), "zipf_s": float(c), "k": int(d),
-                                          "gt_nq": args.gt_nq}
-                                         for a, b, c, d in (x.split(":") for x in args.extra_query_set)])
-    out_dir = args.data_dir or os.path.join("/tmp", f"gann_{spec.name}_{args.nav_n}_{args.builder}")
-    meta_path = os.path.join(out_dir, "meta.json")
-    if os.path.exists(meta_path):
-        meta = json.load(open(meta_path))
-    else:
-        log(f"[bench] building {spec.name} under {out_dir}")
-        meta = gi.build_dataset(spec, out_dir, verbose=True)
-    P = meta["paths"]
-    qk = f"query_{args.query_set}" if args.query_set else "query"
-    if qk not in P:
-        raise SystemExit(f"query set {args.query_set!r} was not built with this index")
-    Q = gi.read_vecs(P[qk], np.uint8 if u8 else np.float32).astype(np.float32)
-    gt = gi.read_vecs(P[f"gt_{args.query_set}" if args.query_set else "gt"], np.int32)
-    g = GustANN(UINT8 if u8 else FLOAT)
-    g.init_pure_mem(GustANNConfig(P["index"], P["pq"], P["nav"]), args.placement == "hbm")
-    D, M, s_el = args.dim, args.M, (1 if u8 else 4)
-    dev = torch.device("cuda:0")
-    rep = args.repeat
-    Qr = np.tile(Q, (rep, 1))
-    nq = Qr.shape[0]
-    q_dev = torch.from_numpy(Qr).to(dev)
-    ent = torch.empty(nq, dtype=torch.int32, device=dev)
-    nns = torch.empty((nq, K), dtype=torch.int32, device=dev)
-    dd = torch.empty((nq, K), dtype=torch.float32, device=dev)
-    mode = {"fused": 0, "stepwise": 1, "lut": 2, "paged": 3, "gp": 4, "uring": 5}[args.mode]
-    fc = torch.empty(nq, dtype=torch.int32, device=dev)
-    ne = torch.empty(nq, dtype=torch.int32, device=dev)
-    na = torch.empty(nq, dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    rows = []
-    for L in args.L:
-        def step():
-            g.search_device(q_dev.data_ptr(), nq, K, L, ent.data_ptr(), nns.data_ptr(), dd.data_ptr(),
-                            fc.data_ptr(), ne.data_ptr(), na.data_ptr(), stream.cuda_stream,
-                            beam_width=args.beam, mode=mode)
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(args.steps):
-            step()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
-        res = nns[: gt.shape[0]].cpu().numpy()
-        rec = recall_at_k(res, gt, K)
-        rec10 = recall_at_k(res, gt, 10) if K > 10 else rec
-        exps = int(ne.sum().item())
-        adcs = int(na.sum().item())
-        alg = exps * (D * s_el + 4) + adcs * (4 + M) + nq * (4 * D + 80)
-        rows.append({"L": L, "ms": ms, "qps": nq / (ms / 1e3), "recall": rec, "recall_at_10": rec10,
-                     "expansions_per_query": exps / nq, "alg_GBps": alg / (ms / 1e3) / 1e9})
-        log(f"[bench] L={L} {ms:.3f} ms qps={nq / (ms / 1e3):.0f} recall@{K}={rec:.4f}")
-    best = next((r for r in rows if r["recall"] >= 0.9), rows[-1])
-    result = {
-        "metric": METRIC, "value": best["qps"], "unit": "queries/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": best["ms"],
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u8/f32" if u8 else "f32",
-        "data": ("synthetic uint8 Gaussian mixture" if u8 else
-                 f"synthetic L2-normalised f32 Gaussian mixture (sigma {sigma})"),
-        "config": {"workload": (f"in_memory_search_{args.n}x{D}_{'u8' if u8 else 'f32'}_M{M}"
-                                + ("" if args.placement == "hbm" else "_host_pinned")
-                                + ("" if args.mode == "fused" else f"_{args.mode}")
-                                + ("" if args.beam == 1 else f"_beam{args.beam}")
-                                + ("" if K == 10 else f"_top{K}")
-                                + ("" if args.zipf <= 0 else f"_zipf{args.zipf}")
-                                + ("" if not args.query_set else f"_queries_{args.query_set}")),
-                   "nq": nq, "L": best["L"], "L_sweep": rows, "index_builder": args.builder,
-                   "index_build_s": meta.get("build_s")},
-        "roofline": {"bound": "hbm", "achieved": best["alg_GBps"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": best["alg_GBps"] / HBM_PEAK_GBS, "traffic": None},
-    }
-    if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import oracle as orc
-        log(f"[bench] CPU baseline (oracle beam search) at L={best['L']}")
-        ix = orc.Index(P["index"], P["pq"], P["nav"], dtype=args.dtype)
-        threads = min(16, os.cpu_count() or 1)
-        n0 = min(256, Q.shape[0])
-        t = time.perf_counter()
-        def cpu_search(Qs):
-            if args.beam > 1:
-                return ix.search_beam(Qs, K, best["L"], args.beam, threads=threads)[:3]
-            return ix.search(Qs, K, best["L"], threads=threads)[:3]
-        cpu_search(Q[:n0])
-        per_q = (time.perf_counter() - t) / n0
-        n = int(min(Q.shape[0], max(n0, args.cpu_seconds / max(per_q, 1e-9))))
-        t = time.perf_counter()
-        on, od, of = cpu_search(Q[:n])
-        dt = time.perf_counter() - t
-        result["cpu_baseline"] = {"value": n / dt, "unit": "queries/s", "cores": threads,
-                                  "kind": "port",
-                                  "sample": f"first {n} queries at L={best['L']}: oracle/gann_oracle.c "
-                                            f"{'orc_search_beam' if args.beam > 1 else 'orc_search'}, "
-                                            f"{threads} threads, {dt:.1f} s"}
-        gn, gd, gf = g.search(Q[:n], n, K, best["L"], beam_width=args.beam)
-        result["parity_sample_bitexact"] = bool(np.array_equal(gn, on) and np.array_equal(gf, of)
-                                                and np.array_equal(gd.view(np.uint32), od.view(np.uint32)))
-    g.close()
-    return result
-
+# ------------------------------------------------------------------ diagnostics
 
 MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8
 
@@ -312,13 +531,13 @@ def bench_knn(args):
                      "unit": "TOP/s", "frac": ops / dt / 1e12 / MFMA_I8_PEAK_TOPS, "traffic": None},
     }
     if not args.no_cpu:
+        cores, model = cpu_info()
         m = max(1, min(nq, 64))
         t = time.perf_counter()
-        c_ids, c_d = gi.brute_force_knn(X, Q[:m], k, threads=min(16, os.cpu_count() or 1))
+        c_ids, c_d = gi.brute_force_knn(X, Q[:m], k, threads=cores)
         cdt = time.perf_counter() - t
-        result["cpu_baseline"] = {"value": m / cdt, "unit": "queries/s",
-                                  "cores": min(16, os.cpu_count() or 1), "kind": "port",
-                                  "sample": f"first {m} queries: gib_brute_force, {cdt:.1f} s"}
+        result["cpu_baseline"] = {"value": m / cdt, "unit": "queries/s", "cores": cores, "kind": "port",
+                                  "sample": f"first {m} queries: gib_brute_force, {cdt:.1f} s; CPU: {model}"}
         result["parity_sample_bitexact"] = bool(np.array_equal(c_ids, ids[:m]) and
                                                 np.array_equal(c_d, d[:m]))
     return result
@@ -410,7 +629,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["adc", "search", "copy", "knn", "gather"], default="adc")
+    ap.add_argument("--workload", choices=["c3", "adc", "search", "copy", "knn", "gather"], default="c3")
     ap.add_argument("--knn-k", type=int, default=100)
     ap.add_argument("--copy-bytes", type=int, default=1 << 31)
     ap.add_argument("--gather-order", default="random",
@@ -419,17 +638,22 @@ def main():
     ap.add_argument("--ids-per-query", type=int, default=4096)
     ap.add_argument("--num-codes", type=int, default=100_000_000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--adc-cpu-seconds", type=float, default=4.0,
+                    help="CPU sample of the ADC microbenchmark nested in the c3 line")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-adc", action="store_true", help="c3: leave out the nested ADC microbenchmark")
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nclusters", type=int, default=1000)
     ap.add_argument("--nav-n", type=int, default=0)
     ap.add_argument("--nq-search", type=int, default=10000)
-    ap.add_argument("--gt-nq", type=int, default=1000)
+    ap.add_argument("--gt-nq", type=int, default=0, help="ground truth for the first N queries (0 = all)")
     ap.add_argument("--repeat", type=int, default=1)
-    ap.add_argument("--L", type=int, nargs="+", default=[32, 48, 64, 96, 128])
+    ap.add_argument("--L", type=int, nargs="+", default=[],
+                    help="search: the L values to time; c3: a fixed L instead of the sweep")
     ap.add_argument("--data-dir", default="")
     ap.add_argument("--dtype", choices=["uint8", "float"], default="uint8")
     ap.add_argument("--dim", type=int, default=128)
+    ap.add_argument("--R", type=int, default=64)
     ap.add_argument("--M", type=int, default=32)
     ap.add_argument("--sigma", type=float, default=0.0, help="0 = 12 (uint8) / 0.05 (float)")
     ap.add_argument("--placement", choices=["hbm", "pinned"], default="hbm")
@@ -448,6 +672,8 @@ def main():
                                    "GPUs with no collective, so one GPU's figure is the unit); "
                                    "--gpus must be 1"}))
         sys.exit(2)
+    if args.workload == "search" and not args.L:
+        args.L = [32, 48, 64, 96, 128]
     import torch
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -455,7 +681,7 @@ def main():
     if args.workload == "copy":
         res = bench_copy(args)
     else:
-        res = {"adc": bench_adc, "search": bench_search, "knn": bench_knn,
+        res = {"c3": bench_c3, "adc": bench_adc, "search": bench_search, "knn": bench_knn,
                "gather": bench_gather}[args.workload](args)
     print(json.dumps(res), flush=True)
 

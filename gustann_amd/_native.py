@@ -14,6 +14,7 @@ ERR_NAMES = {1: "INVALID", 2: "IO", 3: "FORMAT", 4: "HIP", 5: "NOMEM", 6: "UNSUP
 UINT8, FLOAT = 0, 1
 PLACEMENT_HBM, PLACEMENT_HOST_PINNED = 0, 1
 MODE_FUSED, MODE_STEPWISE, MODE_FUSED_LUT, MODE_STEPWISE_PAGED, MODE_FUSED_GP, MODE_STEPWISE_URING = 0, 1, 2, 3, 4, 5
+SEARCH_ENTRIES_GIVEN = 0x100  # OR'ed into a device-entry mode: entries are inputs
 
 # Every symbol declared in include/gustann.h.
 ABI_SYMBOLS = (

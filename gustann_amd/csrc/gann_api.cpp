@@ -1022,9 +1022,10 @@ int gann_search_device_ex(gann_handle* h, const float* q_dev, int32_t nq, int32_
     GANN_HIP(hipSetDevice(h->device));
     hipStream_t s = (hipStream_t)stream;
     SearchScratch sc{h};
-    run_entries(h, q_dev, nq, entries_dev, nullptr, sc.counters(), s);
-    run_search(h, sc, q_dev, nq, topk, L, mode, entries_dev, nns_dev, dists_dev, found_dev, n_exp_dev,
-               n_adc_dev, s, beam_width);
+    if (!(mode & GANN_SEARCH_ENTRIES_GIVEN))
+      run_entries(h, q_dev, nq, entries_dev, nullptr, sc.counters(), s);
+    run_search(h, sc, q_dev, nq, topk, L, mode & ~GANN_SEARCH_ENTRIES_GIVEN, entries_dev, nns_dev,
+               dists_dev, found_dev, n_exp_dev, n_adc_dev, s, beam_width);
   });
 }
 
@@ -1035,6 +1036,8 @@ int gann_search_device_noalloc(gann_handle* h, const float* q_dev, int32_t nq, i
   return guarded([&] {
     if (!h) raise(GANN_ERR_INVALID, "handle is NULL");
     validate_search(h, nq, topk, L, beam_width);
+    const bool given = (mode & GANN_SEARCH_ENTRIES_GIVEN) != 0;
+    mode &= ~GANN_SEARCH_ENTRIES_GIVEN;
     if (mode != GANN_MODE_FUSED && mode != GANN_MODE_FUSED_GP && mode != GANN_MODE_FUSED_LUT)
       raise(GANN_ERR_UNSUPPORTED, "gann_search_device_noalloc runs the fused modes only "
                                   "(GANN_MODE_FUSED, GANN_MODE_FUSED_GP, GANN_MODE_FUSED_LUT)");
@@ -1053,7 +1056,7 @@ int gann_search_device_noalloc(gann_handle* h, const float* q_dev, int32_t nq, i
     hipStream_t s = (hipStream_t)stream;
     uint8_t* base = (uint8_t*)h->noalloc_scratch;
     SearchScratch sc{h, (int32_t*)base, (float*)(base + gann::kNoAllocCounterBytes)};
-    run_entries(h, q_dev, nq, entries_dev, nullptr, sc.counters(), s);
+    if (!given) run_entries(h, q_dev, nq, entries_dev, nullptr, sc.counters(), s);
     run_search(h, sc, q_dev, nq, topk, L, mode, entries_dev, nns_dev, dists_dev, found_dev, n_exp_dev,
                n_adc_dev, s, beam_width);
   });

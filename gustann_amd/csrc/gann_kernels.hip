@@ -306,6 +306,7 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
 
   int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
+  if (u >= ix.num_pts) u = -1;  // caller-given entries outside the index: empty result
   RecRegs<T, kMaxDimRegs> cur;
   if (u >= 0) cur.load(ix, u);
 
@@ -568,6 +569,7 @@ __global__ __launch_bounds__(1024) void search_cb_kernel(IndexDev ix, PQDev pq,
     qi = __builtin_amdgcn_readfirstlane(__shfl(qi, 0, kWave));
     if (qi >= nq) break;
     int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
+    if (u >= ix.num_pts) u = -1;  // caller-given entries outside the index: empty result
     RecRegs<T, KP> cur;
     if (u >= 0) cur.load(ix, u);
     const float* qs = qs_all + (int64_t)qi * dim;  // q - mu, uniform reads
@@ -676,7 +678,7 @@ __global__ __launch_bounds__(1024) void search_beam_kernel(IndexDev ix, PQDev pq
 #pragma unroll
     for (int b = 0; b < kMaxBeam; ++b) sel[b] = -1;
     sel[0] = __builtin_amdgcn_readfirstlane(entries[qi]);
-    int nsel = sel[0] >= 0 ? 1 : 0;
+    int nsel = sel[0] >= 0 && sel[0] < ix.num_pts ? 1 : 0;
     while (nsel > 0) {
       RecRegs<T, KP> rec[kMaxBeam];
 #pragma unroll
@@ -766,7 +768,8 @@ struct StepState {
 // src/hyd_task_runner.cu:12-15) and initialises its state.
 template <int W>
 __global__ __launch_bounds__(64) void step_init_kernel(PQDev pq, const float* __restrict__ q,
-                                                       int nq, const int32_t* __restrict__ entries,
+                                                       int nq, int64_t num_pts,
+                                                       const int32_t* __restrict__ entries,
                                                        float* __restrict__ luts,
                                                        StepState* __restrict__ st) {
   extern __shared__ float qs[];
@@ -776,7 +779,10 @@ __global__ __launch_bounds__(64) void step_init_kernel(PQDev pq, const float* __
   for (int i = lane; i < pq.dim; i += kWave) qs[i] = q[(int64_t)qi * pq.dim + i] - pq.centroid[i];
   __syncthreads();
   lut_build<W>(pq, qs, luts + (int64_t)qi * pq.M * kPivots, lane, kWave);
-  if (lane == 0) st[qi] = StepState{entries[qi], 0, 0, 0, 0, 0};
+  if (lane == 0) {
+    const int32_t e = entries[qi];
+    st[qi] = StepState{e < num_pts ? e : -1, 0, 0, 0, 0, 0};
+  }
 }
 
 // One expansion per active query: the work of merge_data_kernel followed by
@@ -1214,7 +1220,7 @@ hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32
                             float* luts, void* st, hipStream_t stream) {
   return with_w(pq.chunk_w, [&](auto w) {
     hipLaunchKernelGGL((step_init_kernel<decltype(w)::value>), dim3(nq), dim3(64),
-                       (size_t)pq.dim * 4, stream, pq, q, nq, entries, luts,
+                       (size_t)pq.dim * 4, stream, pq, q, nq, pq.num_pts, entries, luts,
                        reinterpret_cast<StepState*>(st));
     return hipGetLastError();
   });

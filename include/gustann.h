@@ -61,6 +61,14 @@ extern "C" {
                                  through the caches and only the lists in LDS, forced (more lists
                                  per CU at large L) */
 
+/* OR'ed into the mode of gann_search_device_ex / gann_search_device_noalloc:
+ * entries_dev holds each query's entry node on input and entry selection is
+ * skipped (a caller that already has entry points, e.g. from another
+ * shard's search, or that times the search kernel alone).  An entry outside
+ * [0, num_pts) gives that query an empty result.  The reference always
+ * selects entries itself (src/pure_mem.cu:104-124). */
+#define GANN_SEARCH_ENTRIES_GIVEN 0x100
+
 typedef struct gann_handle gann_handle;
 typedef struct gann_pq gann_pq;
 

@@ -5,15 +5,43 @@
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -mfma, pthreads).
  */
+#define _GNU_SOURCE
 #include "gann_oracle.h"
 
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdlib.h>
 #include <string.h>
 
 #define MASK31 0x7fffffffu
 #define VISITED 0x80000000u
+
+/* ------------------------------------------------------------------ threads */
+
+static int g_pin_threads = 0;
+
+void orc_set_pin_threads(int32_t on) { g_pin_threads = on != 0; }
+
+/* Worker t of a pool runs on the (t mod n)-th of the n CPUs the process may
+ * use, so a pool of n workers puts one on each core. */
+static void pin_worker(int32_t t) {
+  if (!g_pin_threads) return;
+  cpu_set_t allowed, one;
+  if (sched_getaffinity(0, sizeof allowed, &allowed) != 0) return;
+  const int n = CPU_COUNT(&allowed);
+  if (n <= 0) return;
+  int want = t % n, seen = 0;
+  for (int c = 0; c < CPU_SETSIZE; ++c) {
+    if (!CPU_ISSET(c, &allowed)) continue;
+    if (seen++ == want) {
+      CPU_ZERO(&one);
+      CPU_SET(c, &one);
+      pthread_setaffinity_np(pthread_self(), sizeof one, &one);
+      return;
+    }
+  }
+}
 
 /* ------------------------------------------------------------------ PQ */
 
@@ -68,6 +96,7 @@ typedef struct {
 
 static void* adc_worker(void* arg) {
   adc_job* J = (adc_job*)arg;
+  pin_worker(J->t);
   float* lut = (float*)malloc(sizeof(float) * (size_t)J->num_chunks * ORC_NUM_PIVOTS);
   for (int32_t qi = J->t; qi < J->nq; qi += J->nthreads) {
     orc_lut_build(J->pivots, J->centroid, J->chunk_offsets, J->dim, J->num_chunks,
@@ -414,6 +443,7 @@ typedef struct {
 
 static void* search_worker(void* arg) {
   search_job* J = (search_job*)arg;
+  pin_worker(J->t);
   const orc_index* ix = J->ix;
   int64_t cap = J->L + ix->max_m;
   float* lut = (float*)malloc(sizeof(float) * (size_t)ix->num_chunks * ORC_NUM_PIVOTS);
@@ -551,6 +581,7 @@ typedef struct {
 
 static void* beam_worker(void* arg) {
   beam_job* J = (beam_job*)arg;
+  pin_worker(J->t);
   const orc_index* ix = J->ix;
   float* lut = (float*)malloc(sizeof(float) * (size_t)ix->num_chunks * ORC_NUM_PIVOTS);
   float* qr = (float*)malloc(sizeof(float) * (size_t)ix->dim);

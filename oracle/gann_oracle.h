@@ -103,6 +103,10 @@ int64_t orc_search_beam(const orc_index* ix, const float* q, int32_t nq, const i
                         int32_t topk, int32_t L, int32_t bw, int32_t* nns, float* dists,
                         int32_t* found, int32_t* n_expansions, int32_t nthreads);
 
+/* on != 0: every later call's worker t runs pinned to the (t mod n)-th of
+ * the n CPUs the process may use (the CPU baseline's one thread per core). */
+void orc_set_pin_threads(int32_t on);
+
 /* calc_recall (bin/utils.hpp:104-116): hits of res[i][0..k) in the set of the
  * first k ground-truth ids, over `num` queries, divided by num*k. */
 double orc_recall(const int32_t* res, const int32_t* gt, int32_t num, int32_t gt_dim, int32_t k);

@@ -52,8 +52,31 @@ def lib():
         L.orc_search_beam.restype = I64
         L.orc_recall.argtypes = [P, P, I32, I32, I32]
         L.orc_recall.restype = C.c_double
+        L.orc_set_pin_threads.argtypes = [I32]
+        L.orc_set_pin_threads.restype = None
         _lib = L
     return _lib
+
+
+def set_pin_threads(on: bool):
+    """Pin worker t of every later multi-threaded call to the (t mod n)-th
+    CPU the process may use (one thread per core)."""
+    lib().orc_set_pin_threads(1 if on else 0)
+
+
+def cpu_cores():
+    """(number of CPUs this process may use, CPU model from /proc/cpuinfo)."""
+    n = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return n, model
 
 
 def _p(a):
