@@ -2,7 +2,7 @@
 
   python -m gustann_amd.prof_summary --kernel pq_adc_scan_kernel \\
       --trace DIR [--fetch DIR --write DIR --copy-fetch DIR --copy-write DIR \\
-      --copy-kernel copyBuffer --copy-bytes N --alg-bytes B] [--json OUT]
+      --copy-kernel copyBuffer --copy-bytes N --alg-bytes B] [--meta KEY=VALUE] [--json OUT]
 
 --trace: a `rocprofv3 --kernel-trace --stats --output-format csv` directory
 (average duration of the kernel); --fetch/--write: `--pmc FETCH_SIZE` /
@@ -57,8 +57,13 @@ def main():
     ap.add_argument("--copy-bytes", type=float, default=float(1 << 31))
     ap.add_argument("--alg-bytes", type=float)
     ap.add_argument("--json")
+    ap.add_argument("--meta", action="append", default=[],
+                    help="KEY=VALUE recorded in the summary (e.g. L=2576); integer values as numbers")
     a = ap.parse_args()
     out = {"kernel": a.kernel}
+    for kv in a.meta:
+        k, v = kv.split("=", 1)
+        out[k] = int(v) if v.lstrip("-").isdigit() else v
     if a.trace:
         out["trace"] = kernel_stats(a.trace, a.kernel)
     if a.fetch and a.write:
