@@ -49,9 +49,11 @@ def build_hip(verbose=False):
     objdir = os.path.join(ROOT, "_build")
     os.makedirs(objdir, exist_ok=True)
     from concurrent.futures import ThreadPoolExecutor
-    srcs = ("gann_kernels.hip", "gann_knn.hip", "gann_build.hip", "gann_api.cpp")
+    srcs = ("gann_search_cb_u8.hip", "gann_search_cb_f32.hip", "gann_search_beam_u8.hip",
+            "gann_search_beam_f32.hip", "gann_search_lut.hip", "gann_kernels.hip", "gann_knn.hip",
+            "gann_build.hip", "gann_api.cpp")
     objs = [os.path.join(objdir, src.rsplit(".", 1)[0] + ".o") for src in srcs]
-    with ThreadPoolExecutor(max_workers=len(srcs)) as ex:
+    with ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 4)) as ex:
         for f in [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
                   for src, obj in zip(srcs, objs)]:
             f.result()

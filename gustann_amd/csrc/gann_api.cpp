@@ -418,10 +418,8 @@ void validate_search(const gann_handle* h, int32_t nq, int32_t topk, int32_t L, 
   if (beam > gann::max_beam_width())
     raise(GANN_ERR_UNSUPPORTED, "beam_width must be in [1, " + std::to_string(gann::max_beam_width()) +
                                     "] (1 = the reference's one node per iteration)");
-  if (h->layout.max_m > 64)
-    raise(GANN_ERR_UNSUPPORTED, "graph degree R > 64 is not supported by the wave64 kernels");
-  if (h->layout.dim > 256)
-    raise(GANN_ERR_UNSUPPORTED, "dim > 256 is not supported by the register rerank");
+  if (h->layout.max_m > 128)
+    raise(GANN_ERR_UNSUPPORTED, "graph degree R > 128 is not supported (two 64-neighbour blocks per expansion)");
 }
 
 // Entry selection (src/pure_mem.cu:104-124): nav kernel + on-device
@@ -783,8 +781,9 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
   // as many lists as fit; below kMinLdsWaves lists, the pivots are read
   // through the caches and the LDS holds lists only.
   constexpr int kMinLdsWaves = 8;
-  const int w_lds = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, false);
-  const int w_gp = gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true);
+  const int M = h->pq.dev.M, cw = h->pq.dev.chunk_w, D = (int)Ly.dim;
+  const int w_lds = gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, false, 0);
+  const int w_gp = gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, true, 0);
   if (beam > 1) {
     // beam search: shared-codebook kernel only
     if (mode != GANN_MODE_FUSED && mode != GANN_MODE_FUSED_GP)
@@ -807,12 +806,13 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
     // not in LDS are read through the caches.
     constexpr int kSplitWaves = 11;
     const int chunk_w = h->pq.dev.chunk_w;
-    const int groups = gann::search_cb_split_groups(h->pq.dev.M, chunk_w);
+    // split forms: one 64-neighbour block per expansion only (R <= 64)
+    const int groups = Ly.max_m <= 64 ? gann::search_cb_split_groups(h->pq.dev.M, chunk_w) : 0;
     bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
     int g = 0;
     if (mode == GANN_MODE_FUSED && w_lds < kSplitWaves && groups > 1) {
       for (int c : {groups - 1, groups / 2})
-        if (gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true, c, chunk_w) >= kSplitWaves) {
+        if (gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, true, c) >= kSplitWaves) {
           g = c;
           gp = true;
           break;
@@ -832,7 +832,7 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
         gp = true;
       }
     }
-    const int waves = gp ? gann::search_cb_waves((int)Ly.dim, L, topk, h->lds_limit, true, g, chunk_w) : w_lds;
+    const int waves = gp ? gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, true, g) : w_lds;
     if (waves >= 1 && (gp || waves >= 2)) {
       int32_t* ctr = sc.counters();
       float* qs = sc.qs((int64_t)nq * Ly.dim);

@@ -30,10 +30,11 @@ hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const f
                          const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                          int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
 // Shared-codebook search: waves per workgroup that fit the LDS (0 = does not
-// fit), with the pivot table in LDS or (global_pivots) read from pq.piv_cb,
-// the first lds_groups groups of 8 chunks (chunk_w dims each) still in LDS.
-int search_cb_waves(int dim, int L, int topk, size_t lds_limit, bool global_pivots = false,
-                    int lds_groups = 0, int chunk_w = 0);
+// fit) and the kernel's register budget, with the pivot table in LDS or
+// (global_pivots) read from pq.piv_cb, the first lds_groups groups of 8
+// chunks (chunk_w dims each) still in LDS.
+int search_cb_waves(int dim, int M, int chunk_w, int L, int topk, size_t lds_limit, bool global_pivots,
+                    int lds_groups);
 // Groups of 8 chunks of the pivot table (0: the split forms are not
 // available); the split forms keep all but the last group, or the first
 // half of the groups, in LDS (lds_groups = groups - 1 or groups / 2).

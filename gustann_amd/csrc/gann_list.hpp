@@ -195,6 +195,34 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
   return nfu;
 }
 
+// The plan of one expansion whose neighbours come in NB blocks of 64 (block
+// b holds neighbours 64b .. 64b+63 in key[b], ~0 past deg; graph degree up
+// to 64 NB).  Every block but the last non-empty one is inserted without a
+// selection (list_apply<false>), then the last block is planned as usual.
+// This is the list the reference's single merge of all deg neighbours gives
+// (src/impl/pure_mem.cuh:314-419): the list is always the first L of the
+// sorted union of everything listed so far (an id once, with the listed
+// copy's visited flag), and the first L of (the first L of A ∪ B) ∪ C is the
+// first L of A ∪ B ∪ C; a neighbour list holds no id twice, so no block
+// duplicates another's entry, and the first unvisited entry is carried from
+// block to block (list_apply<false> returns it).  sz and fu are updated for
+// the blocks applied here; the caller applies the returned plan.
+template <int NB>
+__device__ __forceinline__ ListPlan list_plan_nb(uint64_t* A, uint32_t* BM, int L,
+                                                 const uint64_t (&key)[NB], int deg, int& sz,
+                                                 int& fu) {
+  static_assert(NB == 1 || NB == 2, "one or two neighbour blocks");
+  if constexpr (NB == 2) {
+    if (deg > kWave) {
+      const ListPlan P0 = list_plan(A, L, key[0], kWave, sz, fu);
+      fu = list_apply<false>(A, BM, P0);
+      sz = P0.nsz;
+      return list_plan(A, L, key[1], deg - kWave, sz, fu);
+    }
+  }
+  return list_plan(A, L, key[0], min(deg, kWave), sz, fu);
+}
+
 // Top-k insertion of (d, id) into the sorted LDS list (src/impl/util.cuh:116-163):
 // the value lands after the last element that is not greater than it,
 // greater elements shift right, the list keeps at most k.

@@ -153,7 +153,9 @@ def test_search_recall_matches_host_graph(mix, tmp_path):
     X, Q = mix
     pq = gi.train_pq(X, 32, 20000, 8, 2, threads=8)
     g = gi.build_vamana_gpu(X, 32, 64, 1.2, seed=3)
-    c = gi.build_vamana(X, 32, 64, 1.2, 3, threads=8)
+    # the sequential host build (one thread) is deterministic; with several
+    # threads its recall at L = 16 varies by about 0.03 from run to run
+    c = gi.build_vamana(X, 32, 64, 1.2, 3, threads=1)
     _check_graph(g[0], g[1], X.shape[0], 32)
     for L in (16, 48, 160):
         rg = _recall(X, Q, *g, pq, 10, L, str(tmp_path / "gpu"))
