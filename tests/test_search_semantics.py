@@ -66,7 +66,9 @@ def random_graph(rng, n, R, min_deg=1):
                                                            (3, 8, 24, 10, True, 1),
                                                            (4, 16, 6, 6, False, 1),
                                                            (5, 10, 40, 20, True, 1),
-                                                           (6, 10, 12, 5, False, 0)])
+                                                           (6, 10, 12, 5, False, 0),
+                                                           (7, 100, 40, 10, True, 1),
+                                                           (8, 128, 150, 10, False, 60)])
 def test_oracle_search_matches_sort_restatement(tmp_path, seed, R, L, topk, trained, min_deg):
     rng = np.random.default_rng(seed)
     n, D = 240, 16
