@@ -5,10 +5,14 @@
 //
 //   search_mem --query Q --index I --pq_data P [--nav_graph N] --data_type uint8|float
 //              [--ground_truth GT] [--topk K] --ef_search L [L ...] [-R n] [-G]
-//              [--mode fused|lut|stepwise|paged] [--device d] [--result_path FILE]
+//              [--mode fused|gp|lut|stepwise|paged|uring] [--beam_width W] [--device d]
+//              [--result_path FILE]
 //
-// --result_path (an addition) writes the ids of the first L's run as a bin
-// file [nq x topk] int32, the input of check_recall.
+// Additions: --mode selects the execution mode (GANN_MODE_*), --beam_width
+// the beam search of this library (1, the default, is the reference's one
+// node per iteration; 2..4 expand that many list entries per round), and
+// --result_path writes the ids of the first L's run as a bin file
+// [nq x topk] int32, the input of check_recall.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -47,7 +51,8 @@ void usage() {
                "Usage: search_mem --query FILE --index FILE --pq_data PREFIX --data_type uint8|float\n"
                "                  --ef_search L [L ...] [--ground_truth FILE] [--topk K]\n"
                "                  [--nav_graph DIR] [--repeat|-R N] [--use-gpu-mem|-G]\n"
-               "                  [--mode fused|lut|stepwise|paged] [--device D] [--result_path FILE]\n");
+               "                  [--mode fused|gp|lut|stepwise|paged|uring] [--beam_width W]\n"
+               "                  [--device D] [--result_path FILE]\n");
 }
 
 }  // namespace
@@ -58,6 +63,7 @@ int main(int argc, char** argv) {
   int topk = 100;  // bin/search_disk.cpp:29
   int repeat = 20; // :36
   int device = 0;
+  int beam_width = 1;
   bool use_gpu_mem = false;
   std::vector<int> ef;
   for (int i = 1; i < argc; ++i) {
@@ -77,6 +83,7 @@ int main(int argc, char** argv) {
     else if (a == "--use-gpu-mem" || a == "-G") use_gpu_mem = true;
     else if (a == "--mode") mode_s = need("--mode");
     else if (a == "--device") device = std::atoi(need("--device").c_str());
+    else if (a == "--beam_width") beam_width = std::atoi(need("--beam_width").c_str());
     else if (a == "--result_path") result_path = need("--result_path");
     else if (a == "--ef_search") {
       while (i + 1 < argc && argv[i + 1][0] != '-') ef.push_back(std::atoi(argv[++i]));
@@ -98,9 +105,12 @@ int main(int argc, char** argv) {
   else die("unrecognized data type " + data_type);
   int mode = GANN_MODE_FUSED;
   if (mode_s == "lut") mode = GANN_MODE_FUSED_LUT;
+  else if (mode_s == "gp") mode = GANN_MODE_FUSED_GP;
   else if (mode_s == "stepwise") mode = GANN_MODE_STEPWISE;
   else if (mode_s == "paged") mode = GANN_MODE_STEPWISE_PAGED;
+  else if (mode_s == "uring") mode = GANN_MODE_STEPWISE_URING;
   else if (mode_s != "fused") die("unknown --mode " + mode_s);
+  if (beam_width < 1) die("--beam_width must be >= 1 (1 = the reference's one node per iteration)");
   if (ef.empty()) die("--ef_search needs at least one value");
   for (int L : ef)
     if (L < topk) die("ef_search must be >= topk (bin/search_disk.cpp:189-192)");
@@ -141,7 +151,7 @@ int main(int argc, char** argv) {
   if (have_gt && gt_nq > total) die("ground truth has more rows than queries");
 
   auto run = [&](int L, gann_stats* st) {
-    check(gann_search_ex(h, qr.data(), (int32_t)total, topk, L, 1, mode, nns.data(), dis.data(),
+    check(gann_search_ex(h, qr.data(), (int32_t)total, topk, L, beam_width, mode, nns.data(), dis.data(),
                          found.data(), nullptr, st),
           "gann_search");
   };

@@ -67,3 +67,31 @@ def exact_pq(X):
     piv = np.repeat(np.arange(256, dtype=np.float32)[:, None], dim, axis=1)
     return PQTables(piv, np.zeros(dim, np.float32), np.arange(dim + 1, dtype=np.int32),
                     np.ascontiguousarray(X.astype(np.uint8)))
+
+
+# A 12-node line graph worked by hand for the beam search: node i sits at
+# x = BEAM_X[i] on the first axis (the other 3 dims 0), the query at the
+# origin, the PQ exact (exact_pq), so every ADC and exact distance is x^2;
+# entry node 0, list L = 4, top-3.  Each round takes the first `width`
+# unvisited entries (marking them visited), then expands them in list order,
+# each expansion inserting its unlisted neighbours (cut back to 4 entries)
+# and pushing its own distance into the top-3.  The traces:
+#   width 1 (the reference search): expands 0, 1, 3, 5, 7, 8 -> 6 expansions,
+#     top-3 ids 8, 7, 5 (1, 4, 16);
+#   width 2: rounds {0}, {1, 9}, {3, 2}, {5, 4}, {7, 6}, {8} -> 10 expansions,
+#     top-3 ids 8, 7, 6 (1, 4, 9);
+#   width 4: rounds {0}, {1, 9, 10}, {3, 2}, {5, 4}, {7, 6}, {8} -> 11
+#     expansions, top-3 8, 7, 6.
+# In the last round the list is [8, 7*, 6*, 5*] (width 2 and 4): a selection
+# that did not mark its nodes visited would take 7 again.
+BEAM_X = [10, 8, 7, 6, 5, 4, 3, 2, 1, 9, 11, 12]
+BEAM_ADJ = [[1, 9, 10], [2, 3, 0], [4, 11], [5, 1], [6], [7, 2], [8], [8, 3], [7], [0, 2], [11], [10]]
+BEAM_EXPECT = {1: (6, [8, 7, 5], [1.0, 4.0, 16.0]),
+               2: (10, [8, 7, 6], [1.0, 4.0, 9.0]),
+               4: (11, [8, 7, 6], [1.0, 4.0, 9.0])}
+
+
+def write_beam_known_answer_index(d):
+    X = np.zeros((len(BEAM_X), 4), np.uint8)
+    X[:, 0] = BEAM_X
+    return write_custom_index(d, X, BEAM_ADJ, 0, 3)

@@ -95,3 +95,20 @@ def test_beam_limits(u8):
         g.search(Q, 4, 10, 40, beam_width=2, mode=MODE_STEPWISE)
     nns, _, f = g.search(Q, 4, 10, 40, beam_width=2, mode=MODE_FUSED)
     assert (f == 10).all()
+
+
+@pytest.mark.parametrize("bw", [1, 2, 4])
+@pytest.mark.parametrize("mode", [MODE_FUSED, MODE_FUSED_GP])
+def test_beam_known_answers(tmp_path, bw, mode):
+    # the hand-worked traces of tests/_helpers.py (BEAM_EXPECT) on the kernel
+    from _helpers import BEAM_EXPECT, write_beam_known_answer_index
+    paths = write_beam_known_answer_index(str(tmp_path))
+    g = GustANN(UINT8)
+    g.init_pure_mem(GustANNConfig(paths[0], paths[1], ""), True)
+    q = np.zeros((1, 4), np.float32)
+    nexp, ids, dists = BEAM_EXPECT[bw]
+    ne = np.empty(1, np.int32)
+    nns, d, f = g.search(q, 1, 3, 4, beam_width=bw, n_exp=ne, mode=mode)
+    g.close()
+    assert ne[0] == nexp and f[0] == 3
+    assert nns[0].tolist() == ids and d[0].tolist() == dists

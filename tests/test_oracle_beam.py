@@ -1,8 +1,9 @@
 """The oracle's beam search (orc_search_beam) against the reference
 restatement: with beam width 1 it is the same algorithm as orc_search (the
 reference's one node per iteration), so every output must be identical; with
-wider beams it must still return exact distances in order and a recall close
-to width 1's."""
+wider beams it must reproduce the hand-worked traces of a 12-node graph
+(expansion counts and top-k at widths 1, 2 and 4) and still return exact
+distances in order and a recall close to width 1's."""
 import numpy as np
 import pytest
 
@@ -35,3 +36,19 @@ def test_wider_beam_exact_and_sorted(tiny_u8, bw):
     rb = orc.recall(nns, gt, 10)
     assert rb >= r1 - 0.05
     assert (nexp > 0).all()
+
+
+@pytest.mark.parametrize("bw", [1, 2, 4])
+def test_beam_known_answers(tmp_path, bw):
+    # the hand-worked traces of tests/_helpers.py (BEAM_EXPECT)
+    from _helpers import BEAM_EXPECT, write_beam_known_answer_index
+    paths = write_beam_known_answer_index(str(tmp_path))
+    ix = orc.Index(*paths[:2])
+    q = np.zeros((1, 4), np.float32)
+    nexp, ids, dists = BEAM_EXPECT[bw]
+    nns, d, found, ne = ix.search_beam(q, 3, 4, bw)
+    assert ne[0] == nexp and found[0] == 3
+    assert nns[0].tolist() == ids and d[0].tolist() == dists
+    if bw == 1:
+        rn, rd, rf, re, _ = ix.search(q, 3, 4)
+        assert re[0] == nexp and rn[0].tolist() == ids and rd[0].tolist() == dists
