@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void random_graph_kernel(BuildDev g, int init_
 // ------------------------------------------------------------------ build search
 
 __host__ __device__ inline size_t search_wave_bytes(int L) {
-  const size_t b = (size_t)L * 8 + (size_t)list_scratch_words(L) * 4 + (size_t)kBuildPoolMax * 8;
+  const size_t b = (size_t)list_capacity(L) * 8 + (size_t)list_scratch_words(L) * 4 + (size_t)kBuildPoolMax * 8;
   return (b + 15) & ~(size_t)15;
 }
 
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void build_search_kernel(BuildDev g, const uin
   const int lane = lane_id();
   uint8_t* wbase = smem_raw + (size_t)(threadIdx.x >> 6) * search_wave_bytes(L);
   uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
-  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + list_capacity(L));
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + kBuildPoolMax);
   const int64_t cap = g.n + 2;

@@ -33,12 +33,17 @@ namespace gann {
 // node's record between them: plan() ranks the new run and picks the next
 // node without writing; apply() shifts the list in place (top chunk first,
 // skipping everything below the first insertion) and marks the node visited.
-// A: the list (sorted by key, distinct ids, visited flag in bit 31 of the low
-// word), capacity >= L; BM: list_scratch_words(L) words of scratch.
+// A: the list (sorted by key, distinct ids, visited flag in bit 0), of
+// list_capacity(L) entries; BM: list_scratch_words(L) words of scratch.
 
 // Scratch words per wave for the list update: a bitmap of the positions the
 // inserted entries take, two words per 64-entry chunk.
 __host__ __device__ constexpr int list_scratch_words(int L) { return 2 * ((L + kWave - 1) / kWave); }
+
+// Entries allocated for a list of at most L: L rounded up to whole 64-entry
+// chunks, so that every lane of a chunk the update touches is inside the
+// wave's own list.
+__host__ __device__ constexpr int list_capacity(int L) { return (L + kWave - 1) / kWave * kWave; }
 
 // Rank of `key` in the sorted list A[0..sz): the number of entries ordered
 // below it.  A first level shared by all lanes splits the list into 9
@@ -126,14 +131,16 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
 // Applies the plan in place and returns the new first-unvisited index.  The
 // positions the inserted entries take are marked in the bitmap BM; output
 // position j then holds inserted entry nb(j) (nb = inserted entries placed
-// before j) if marked, else old entry j - nb(j).  Outputs are gathered in
-// batches of 8 chunks, top batch first: a batch reads only positions at or
-// above its lowest output minus 64 and writes after all its reads, so no
-// source is overwritten before it is read.
+// before j) if marked, else old entry j - nb(j).  The old entries are
+// gathered into the unmarked positions in batches of 16 chunks, top batch
+// first: a batch reads only positions below its highest output and at or
+// above its lowest output minus 64, and writes after all its reads, so no
+// source is overwritten before it is read; then each inserted entry is stored
+// at its marked position by the lane that holds it.
 // kSelect = false (beam search) only applies the insertions and returns P.lb.
 template <bool kSelect = true>
 __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListPlan& P) {
-  constexpr int kBatch = 8;
+  constexpr int kBatch = 16;
   const int lane = lane_id();
   wave_sync();  // all reads of plan() done
   const int start = min(P.p0, P.nsz);
@@ -143,41 +150,50 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
     const int w_lo = ob_lo / 32;
     for (int w = lane; w < 2 * nch; w += kWave) BM[w_lo + w] = 0u;
     wave_sync();
-    if (lane < P.n_nd && P.p < P.nsz) atomicOr(&BM[P.p >> 5], 1u << (P.p & 31));
+    const bool placed = lane < P.n_nd && P.p < P.nsz;
+    if (placed) atomicOr(&BM[P.p >> 5], 1u << (P.p & 31));
+    // positions from nsz to the end of the top chunk are marked as well, so
+    // that they keep their entries like the inserted positions do
+    const int jt = ob_lo + kWave * (nch - 1) + lane;
+    if (jt >= P.nsz) atomicOr(&BM[jt >> 5], 1u << (jt & 31));
+    const int n_tail = ob_lo + kWave * nch - P.nsz;
+    // inserted entries placed below the end of the current chunk, counted
+    // down from the top chunk
+    int below = __popcll(ballot64(placed));
+    const uint64_t lanebit = 1ull << lane;
     wave_sync();
-    const uint32_t klo = (uint32_t)P.nkey, khi = (uint32_t)(P.nkey >> 32);
     for (int b_hi = nch; b_hi > 0; b_hi -= kBatch) {
       const int b_lo = max(0, b_hi - kBatch);
       const uint32_t wv = lane < 2 * (b_hi - b_lo) ? BM[w_lo + 2 * b_lo + lane] : 0u;
+      // straight-line: every lane reads one entry and writes one back, with
+      // no branch between the reads and the writes (a lane whose output does
+      // not move -- a marked position -- rewrites its own entry; slots past
+      // the bottom of the batch repeat its bottom chunk, the same reads and
+      // writes twice)
       uint64_t val[kBatch];
+      int dst[kBatch];
 #pragma unroll
       for (int t = 0; t < kBatch; ++t) {
-        val[t] = 0;
-        if (b_lo + t < b_hi) {
-          const int ob = ob_lo + kWave * (b_lo + t);
-          uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * t + 1) << 32) |
-                        (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * t);
-          const int valid = P.nsz - ob;
-          if (valid < kWave) mo &= (1ull << valid) - 1;
-          const int nb = __popcll(ballot64(lane < P.n_nd && P.p < ob)) + rank_below(mo);
-          const bool isnew = (mo >> lane) & 1;
-          const int src = nb & (kWave - 1);
-          const uint32_t nlo = (uint32_t)__shfl((int)klo, src, kWave);
-          const uint32_t nhi = (uint32_t)__shfl((int)khi, src, kWave);
-          const int j = ob + lane;
-          uint64_t ov = 0;
-          if (!isnew && j < P.nsz) ov = A[j - nb];
-          val[t] = isnew ? (((uint64_t)nhi << 32) | nlo) : ov;
-        }
+        const bool rep = b_hi - 1 - t < b_lo;              // uniform
+        const int c = rep ? b_lo : b_hi - 1 - t;           // chunk, top first
+        const int tw = c - b_lo;
+        const uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw + 1) << 32) |
+                            (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw);
+        if (!rep) below -= __popcll(mo) - (c == nch - 1 ? n_tail : 0);  // now: placed below the chunk
+        const int j = ob_lo + kWave * c + lane;
+        const int nb = below + rank_below(mo);
+        dst[t] = j;
+        val[t] = A[(mo & lanebit) ? j : j - nb];
       }
       wave_sync();
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        const int j = ob_lo + kWave * (b_lo + t) + lane;
-        if (b_lo + t < b_hi && j < P.nsz) A[j] = val[t];
-      }
+      for (int t = 0; t < kBatch; ++t) A[dst[t]] = val[t];
       wave_sync();
     }
+    // the inserted entries into their marked positions, after every old
+    // entry has moved out of the way
+    if (placed) A[P.p] = P.nkey;
+    wave_sync();
   }
   if (!kSelect) return P.lb;
   if (P.cand < 0) return P.nsz;

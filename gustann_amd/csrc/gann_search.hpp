@@ -111,7 +111,7 @@ __device__ __forceinline__ void restored_query_regs(const float* q, const float*
 // list scratch | top-k dists | top-k ids.
 struct SearchSmem {
   static __host__ __device__ size_t bytes(int M, int dim, int L, int k) {
-    return (size_t)M * kPivots * 4 + (size_t)((dim + 1) & ~1) * 4 + (size_t)L * 8 +
+    return (size_t)M * kPivots * 4 + (size_t)((dim + 1) & ~1) * 4 + (size_t)list_capacity(L) * 8 +
            (size_t)list_scratch_words(L) * 4 + (size_t)k * 8;
   }
 };
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(64) void search_kernel(IndexDev ix, PQDev pq,
   float* lut = reinterpret_cast<float*>(smem_raw);
   float* qr = lut + M * kPivots;
   uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
-  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + list_capacity(L));
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
 
@@ -256,7 +256,7 @@ struct CbSmem {
   // per-wave bytes: list (L) | list scratch | top-k d, top-k id (LDS only
   // when k > 64; smaller top-k lists live in registers)
   static __host__ __device__ size_t wave_bytes(int L, int k) {
-    size_t b = (size_t)L * 8 + (size_t)list_scratch_words(L) * 4 + (k > kWave ? (size_t)k * 8 : 0);
+    size_t b = (size_t)list_capacity(L) * 8 + (size_t)list_scratch_words(L) * 4 + (k > kWave ? (size_t)k * 8 : 0);
     return (b + 15) & ~(size_t)15;
   }
   static __host__ __device__ size_t pivot_bytes(int dim) { return (size_t)kPivots * cb_stride(4 * dim); }
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(cb_block_threads(KP)) void search_cb_kernel(
   const int wave = threadIdx.x >> 6;
   uint8_t* wbase = smem_raw + lists_at + (size_t)wave * CbSmem::wave_bytes(L, topk);
   uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
-  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + list_capacity(L));
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
   const int64_t cap = ix.num_pts + 2;
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(cb_block_threads(KP)) void search_beam_kernel(
   const int wave = threadIdx.x >> 6;
   uint8_t* wbase = smem_raw + lists_at + (size_t)wave * CbSmem::wave_bytes(L, topk);
   uint64_t* A = reinterpret_cast<uint64_t*>(wbase);
-  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + list_capacity(L));
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
   const int64_t cap = ix.num_pts + 2;
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
   const int dim = ix.dim, M = pq.M, R = ix.R;
   float* qr = reinterpret_cast<float*>(smem_raw);
   uint64_t* A = reinterpret_cast<uint64_t*>(qr + ((dim + 1) & ~1));
-  uint32_t* BM = reinterpret_cast<uint32_t*>(A + L);
+  uint32_t* BM = reinterpret_cast<uint32_t*>(A + list_capacity(L));
   float* td = reinterpret_cast<float*>(BM + list_scratch_words(L));
   int32_t* ti = reinterpret_cast<int32_t*>(td + topk);
   const float* lut = luts + (int64_t)qi * M * kPivots;
@@ -870,7 +870,7 @@ template <typename T>
 hipError_t launch_round_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq, const float* luts,
                           int topk, int L, uint64_t* lists, StepState* st, int32_t* nns, float* dists,
                           int32_t* active, const uint8_t* slots, hipStream_t stream) {
-  const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + (size_t)L * 8 +
+  const size_t smem = (size_t)((ix.dim + 1) & ~1) * 4 + (size_t)list_capacity(L) * 8 +
                       (size_t)list_scratch_words(L) * 4 + (size_t)topk * 8;
   return with_nb(ix.R, [&](auto nb) {
     return with_mw(pq.M, [&](auto mw) {
