@@ -818,8 +818,14 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
           break;
         }
     }
-    // tuning override: "split" (all groups but one in LDS), "half" or
-    // "cache" (none in LDS) forces that form
+    // Once at most 8 lists fit per CU beside no table (L >= ~2000 at dim
+    // 128), the registers of 8-wave workgroups hold every pivot row of a
+    // lookup in flight (the wide form).
+    const bool wide_ok = gann::search_cb_wide_ok(M, cw, D);
+    if (mode == GANN_MODE_FUSED && gp && g == 0 && wide_ok && w_gp <= 8) g = gann::kCbGpWide;
+    // tuning override: "split" (all groups but one in LDS), "half",
+    // "cache" (none in LDS) or "wide" (none in LDS, wide lookup) forces that
+    // form
     if (const char* e = std::getenv("GANN_PIVOT_FORM")) {
       if (!std::strcmp(e, "split") && groups > 1) {
         g = groups - 1;
@@ -829,6 +835,9 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
         gp = true;
       } else if (!std::strcmp(e, "cache")) {
         g = 0;
+        gp = true;
+      } else if (!std::strcmp(e, "wide") && wide_ok) {
+        g = gann::kCbGpWide;
         gp = true;
       }
     }

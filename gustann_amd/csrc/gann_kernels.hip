@@ -358,12 +358,17 @@ int search_cb_waves(int dim, int M, int chunk_w, int L, int topk, size_t lds_lim
   const size_t piv = global_pivots ? split_pivot_bytes(lds_groups, chunk_w) : CbSmem::pivot_bytes(dim);
   const size_t w = CbSmem::wave_bytes(L, topk);
   if (piv + w > lds_limit) return 0;
-  const int cap = cb_block_threads(cb_rerank_regs(M, chunk_w, dim)) / kWave;
+  const int cap = cb_block_threads(cb_rerank_regs(M, chunk_w, dim), global_pivots ? lds_groups : 0) / kWave;
   return (int)std::min<size_t>((size_t)cap, (lds_limit - piv) / w);
 }
 
 int search_cb_split_groups(int M, int chunk_w) {
   return (mw_of(M) > 0 && (chunk_w == 2 || chunk_w == 4)) ? M / 8 : 0;
+}
+
+bool search_cb_wide_ok(int M, int chunk_w, int dim) {
+  const int mw = mw_of(M);
+  return mw > 0 && (chunk_w == 2 || chunk_w == 4) && 16 * mw * chunk_w <= 128 && dim == M * chunk_w;
 }
 
 size_t search_cb_pivot_bytes(int dim) { return CbSmem::pivot_bytes(dim); }
@@ -397,8 +402,11 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
                             hipStream_t stream) {
   if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
   const int split = search_cb_split_groups(pq.M, pq.chunk_w);
-  if (lds_groups != 0 && (!global_pivots || (lds_groups != split - 1 && lds_groups != split / 2)))
+  if (lds_groups == kCbGpWide) {
+    if (!global_pivots || !search_cb_wide_ok(pq.M, pq.chunk_w, ix.dim)) return hipErrorInvalidValue;
+  } else if (lds_groups != 0 && (!global_pivots || (lds_groups != split - 1 && lds_groups != split / 2))) {
     return hipErrorInvalidValue;
+  }
   const size_t smem = (global_pivots ? split_pivot_bytes(lds_groups, pq.chunk_w) : CbSmem::pivot_bytes(ix.dim)) +
                       (size_t)waves * CbSmem::wave_bytes(L, topk);
   hipError_t e = prepare_cb(ix, pq, q, nq, queue, qs_all, stream);

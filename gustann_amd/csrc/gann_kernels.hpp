@@ -39,6 +39,12 @@ int search_cb_waves(int dim, int M, int chunk_w, int L, int topk, size_t lds_lim
 // available); the split forms keep all but the last group, or the first
 // half of the groups, in LDS (lds_groups = groups - 1 or groups / 2).
 int search_cb_split_groups(int M, int chunk_w);
+// lds_groups value (with global_pivots) of the wide form: the whole table
+// read through the caches with every pivot row of a lookup requested at
+// once, in workgroups of at most 8 waves; served where search_cb_wide_ok
+// (16, 32 or 64 chunks of 2 or 4 dims, at most 128 dims).
+constexpr int kCbGpWide = -1;
+bool search_cb_wide_ok(int M, int chunk_w, int dim);
 // Size and contents of pq.piv_cb: the pivots [256][dim] in the kernel's row layout.
 size_t search_cb_pivot_bytes(int dim);
 void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out);

@@ -320,12 +320,46 @@ __device__ __forceinline__ PV lds_at(uint32_t a) {
   return *reinterpret_cast<const __attribute__((address_space(3))) PV*>((size_t)a);
 }
 
-template <int W, int MW, int kSplitG = 0, bool kPivLds = false, bool kSplitLds = false>
+// kWide (pivot table read through the caches, none of it in LDS): the
+// pivot rows of all 16 MW chunks are requested before the first is used, so
+// a lookup waits for one cache round trip instead of one per 8 chunks; the
+// 64 MW W-float rows need the register budget of 8-wave workgroups.
+template <int W, int MW, int kSplitG = 0, bool kPivLds = false, bool kSplitLds = false, bool kWide = false>
 __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uint32_t rowb,
                                         const PQDev& pq, const CodeRow<MW>& row,
                                         const uint8_t* crow, const uint8_t* pivl = nullptr) {
   float dist = 0.0f;
-  if constexpr (MW > 0 && (W == 4 || W == 2)) {
+  if constexpr (kWide) {
+    static_assert(MW > 0 && (W == 4 || W == 2) && kSplitG == 0 && !kPivLds, "wide form: whole table in HBM");
+    typedef typename PivotVec<W>::type PV;
+    constexpr int kM = 16 * MW;
+    PV p[kM];
+#pragma unroll
+    for (int k = 0; k < MW; ++k) {
+      const uint32_t ws[4] = {row.w[k].x, row.w[k].y, row.w[k].z, row.w[k].w};
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        const uint32_t c = (ws[b >> 2] >> (8 * (b & 3))) & 0xffu;
+        p[16 * k + b] = *reinterpret_cast<const PV*>(piv + cb_row(c, rowb) + (16 * k + b) * W * 4);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < kM / 8; ++g) {
+      uint64_t qa = (uint64_t)(qs + 8 * g * W);
+      asm volatile("" : "+s"(qa));
+      const __attribute__((address_space(4))) float* qg = (const __attribute__((address_space(4))) float*)qa;
+      float qv[8 * W];
+#pragma unroll
+      for (int i = 0; i < 8 * W; ++i) qv[i] = qg[i];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        float pv[W];
+#pragma unroll
+        for (int i = 0; i < W; ++i) pv[i] = p[8 * g + b][i];
+        dist = dist + cb_chunk<W>(qv + b * W, pv);
+      }
+    }
+  } else if constexpr (MW > 0 && (W == 4 || W == 2)) {
     typedef typename PivotVec<W>::type PV;
 #pragma unroll
     for (int k = 0; k < MW; ++k) {
@@ -377,17 +411,25 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
   return dist;
 }
 
+constexpr int kGpWide = kCbGpWide;
+
 // Largest workgroup of the shared-codebook kernels: 16 waves, or 8 when a
-// lane keeps more than 8 rerank coordinates (the 128-VGPR cap of 16-wave
-// workgroups would spill them).
-__host__ __device__ constexpr int cb_block_threads(int KP) { return KP > 8 ? 512 : 1024; }
+// lane keeps more than 8 rerank coordinates or all pivot rows of a lookup
+// (kGpWide) in flight (the 128-VGPR cap of 16-wave workgroups would spill
+// them).
+__host__ __device__ constexpr int cb_block_threads(int KP, int kSplitG = 0) {
+  return (KP > 8 || kSplitG == kGpWide) ? 512 : 1024;
+}
 
 // kGP: the pivot table is read from pq.piv_cb (HBM, through the caches)
 // instead of a copy in LDS, which then holds only the per-wave lists: the
 // form for large L, where lists beside a 128 KB table leave few waves.
-// KP: rerank coordinates per lane held in registers; NB: neighbour blocks.
+// kSplitG > 0 (with kGP): that many groups of 8 chunks also in LDS;
+// kSplitG == kGpWide (with kGP): the wide lookup of cb_adc, 8-wave
+// workgroups.  KP: rerank coordinates per lane held in registers; NB:
+// neighbour blocks.
 template <typename T, int MW, int W, bool kGP, int kSplitG, int KP, int NB>
-__global__ __launch_bounds__(cb_block_threads(KP)) void search_cb_kernel(
+__global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kernel(
     IndexDev ix, PQDev pq, const float* __restrict__ q, int nq, const int32_t* __restrict__ entries,
     int topk, int L, int32_t* __restrict__ nns, float* __restrict__ dists,
     int32_t* __restrict__ found_cnt, int32_t* __restrict__ n_exp, int32_t* __restrict__ n_adc,
@@ -457,7 +499,8 @@ __global__ __launch_bounds__(cb_block_threads(KP)) void search_cb_kernel(
           CodeRow<MW> row;
           const uint8_t* crow = pq.codes + (int64_t)cur.v[b] * M;
           row.load(crow, M);
-          key[b] = make_key(cb_adc<W, MW, kSplitG, !kGP, (KP <= 4)>(piv, qs, rowb, pq, row, crow, smem_raw),
+          key[b] = make_key(cb_adc<W, MW, (kSplitG > 0 ? kSplitG : 0), !kGP, (KP <= 4), (kSplitG == kGpWide)>(
+                                piv, qs, rowb, pq, row, crow, smem_raw),
                             cur.v[b]);
         }
       }
@@ -792,12 +835,22 @@ hipError_t launch_search_cb_t(const IndexDev& ix, const PQDev& pq, const float* 
     constexpr int NBv = decltype(nb)::value;
     return with_cb_shape(pq.M, pq.chunk_w, ix.dim, [&](auto mw, auto w, auto kp) {
       constexpr int MWv = decltype(mw)::value, Wv = decltype(w)::value, KPv = decltype(kp)::value;
-      if (waves * kWave > cb_block_threads(KPv)) return hipErrorInvalidConfiguration;
+      if (waves * kWave > cb_block_threads(KPv, lds_groups == kGpWide ? kGpWide : 0))
+        return hipErrorInvalidConfiguration;
       // the split forms keep part of the table in LDS for one neighbour
       // block; with two the extra live registers would spill
       constexpr bool kCanSplit = MWv > 0 && NBv == 1;
       constexpr int kSplit = kCanSplit ? 2 * MWv - 1 : 0, kHalf = kCanSplit ? MWv : 0;
       const dim3 grid(blocks), block(waves * kWave);
+      // the wide form: all 16 MW pivot rows of a lookup in at most 128 registers
+      constexpr bool kCanWide = MWv > 0 && 16 * MWv * Wv <= 128;
+      if constexpr (kCanWide) {
+        if (global_pivots && lds_groups == kGpWide)
+          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kGpWide, KPv, NBv>, [&] {
+            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kGpWide, KPv, NBv>), grid, block, smem, stream,
+                               ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+          });
+      }
       if constexpr (kCanSplit) {
         if (global_pivots && lds_groups > 0 && lds_groups == kSplit)
           return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kSplit, KPv, NBv>, [&] {

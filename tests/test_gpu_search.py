@@ -283,11 +283,12 @@ def test_zero_degree_nodes_match_oracle(tmp_path, seed):
     g.close()
 
 
-@pytest.mark.parametrize("form", ["split", "half", "cache"])
+@pytest.mark.parametrize("form", ["split", "half", "cache", "wide"])
 def test_pivot_table_forms_match_oracle(u8, form, monkeypatch):
     # all but the last group of 8 chunks of the pivot table in LDS ("split"),
     # its first half ("half"), or the whole table read through the caches
-    # ("cache"); GANN_PIVOT_FORM forces the form at every L
+    # ("cache"), with all 32 pivot rows of a lookup requested at once in
+    # 8-wave workgroups ("wide"); GANN_PIVOT_FORM forces the form at every L
     meta, g, ix = u8
     Q = _queries(meta)
     monkeypatch.setenv("GANN_PIVOT_FORM", form)
@@ -296,6 +297,36 @@ def test_pivot_table_forms_match_oracle(u8, form, monkeypatch):
         got = g.search(Q, Q.shape[0], topk, L, n_exp=ne)
         on, od, of, oe, _ = ix.search(Q, topk, L, threads=8)
         _assert_same(got, (on, od, of), ne, oe)
+
+
+@pytest.mark.parametrize("dtype,D,M,R", [("uint8", 32, 16, 64), ("uint8", 64, 16, 40), ("uint8", 64, 32, 64),
+                                         ("float", 96, 48, 64), ("uint8", 128, 64, 48), ("uint8", 128, 32, 100)])
+def test_wide_lookup_form_matches_oracle(tmp_path, monkeypatch, dtype, D, M, R):
+    # the wide lookup form on each shape it serves (16 to 64 chunks of 2 or
+    # 4 dims, at most 128 dims), one or two neighbour blocks, ragged degrees
+    # down to 0 and a full-degree entry node, against the oracle
+    rng = np.random.default_rng(D * 7 + M + R)
+    n = 600
+    if dtype == "uint8":
+        X = rng.integers(0, 256, (n, D)).astype(np.uint8)
+        Q = rng.integers(0, 256, (48, D)).astype(np.float32)
+    else:
+        X = rng.standard_normal((n, D)).astype(np.float32)
+        Q = rng.standard_normal((48, D)).astype(np.float32)
+    adj = random_graph(rng, n, R, min_deg=0)
+    adj[1] = [int(v) for v in rng.choice(np.arange(2, n), size=R, replace=False)]
+    pq = gi.train_pq(X, M, sample=n, iters=4, seed=D + M)
+    paths = write_custom_index(str(tmp_path), X, adj, 1, R, pq=pq)
+    g = _open(paths, dtype=UINT8 if dtype == "uint8" else FLOAT, nav=False)
+    ix = orc.Index(*paths[:2], "", dtype)
+    monkeypatch.setenv("GANN_PIVOT_FORM", "wide")
+    for L, topk in ((12, 5), (64, 10), (300, 100)):
+        on, od, of, oe, _ = ix.search(Q, topk, L)
+        ne = np.empty(48, np.int32)
+        got = g.search(Q, 48, topk, L, n_exp=ne, mode=MODE_FUSED)
+        _assert_same(got, (on, od, of), ne, oe)
+    monkeypatch.delenv("GANN_PIVOT_FORM", raising=False)
+    g.close()
 
 
 @pytest.mark.parametrize("dtype,D,M", [("uint8", 192, 48), ("uint8", 256, 64), ("float", 192, 48)])
