@@ -299,7 +299,7 @@ def bench_c3(args):
                    "dataset_ready_s": build_s, "timed_wall_s": wall},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "alg_bytes_per_launch": alg,
-                     "kernel": "search_cb_kernel (fused beam search, pivot table through the caches)"},
+                     "kernel": "search_cb_kernel (fused beam search; pivot table through the caches, wide lookup at L >= ~2000)"},
     }
     if not args.no_cpu:
         log(f"[bench] CPU baseline (oracle) at L={L}")
