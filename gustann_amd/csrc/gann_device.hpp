@@ -206,6 +206,31 @@ __device__ __forceinline__ void wave_sort64_kv(uint64_t& key, uint32_t& val) {
   bitonic_merge<64, 32>(key, val);
 }
 
+// The same ordering for few keys: `live` (uniform) marks the lanes whose key
+// is not ~0.  Each live lane counts the live keys below its own (one
+// readlane pair and one compare per live lane; equal keys, which the callers
+// never have, are ordered by lane so the positions stay a permutation), the
+// other lanes take the positions after them in lane order, and one forward
+// permute per 32-bit word moves every pair to its position.  About 5 VALU
+// per live lane against ~170 for the bitonic network, so the cheaper form
+// up to kFewSort live keys.  Every lane must be active.
+constexpr int kFewSort = 16;
+__device__ __forceinline__ void wave_sort_few_kv(uint64_t& key, uint32_t& val, uint64_t live) {
+  int pos = 0;
+  for (uint64_t m = live; m != 0; m &= m - 1) {
+    const int l = (int)__builtin_ctzll(m);
+    const uint64_t kl = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), l) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, l);
+    pos += (kl < key || (kl == key && l < lane_id())) ? 1 : 0;
+  }
+  if (!((live >> lane_id()) & 1)) pos = __popcll(live) + rank_below(~live);
+  const int a = pos << 2;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_permute(a, (int)(uint32_t)key);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_permute(a, (int)(uint32_t)(key >> 32));
+  val = (uint32_t)__builtin_amdgcn_ds_permute(a, (int)val);
+  key = ((uint64_t)hi << 32) | lo;
+}
+
 // The shfl_down tree 16/8/4/2/1 of square_sum_32 (src/impl/util.cuh:36-45)
 // over the partials of lanes 0..31, read at lane 0 and returned to every
 // lane.  The xor butterfly adds the same operand pairs as shfl_down for the

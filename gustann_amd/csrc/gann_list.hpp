@@ -107,7 +107,13 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
   const bool dup = active && (int)r < sz && entry_id(A[r]) == entry_id(key);
   if (!active || dup || (int)r >= L) key = ~(uint64_t)0;  // never a real key: ids are < 2^31 - 1
   const uint64_t live = ballot64(key != ~(uint64_t)0);
-  if (live != 0) wave_sort64_kv(key, r);  // uniform branch; the sort keeps the count
+  // uniform branches; the sort keeps the count
+  if (live != 0) {
+    if (__popcll(live) <= kFewSort)
+      wave_sort_few_kv(key, r, live);
+    else
+      wave_sort64_kv(key, r);
+  }
   ListPlan P;
   P.nkey = key;
   P.n_nd = __popcll(live);
