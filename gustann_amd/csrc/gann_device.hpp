@@ -366,6 +366,11 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int MW>
 struct CodeRow {
   u32x4 w[MW > 0 ? MW : 1];
+  // all codes 0 (lanes without a neighbour: their lookups stay in bounds)
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int k = 0; k < (MW > 0 ? MW : 1); ++k) w[k] = u32x4{0u, 0u, 0u, 0u};
+  }
   __device__ __forceinline__ void load(const uint8_t* row, int M) {
     if constexpr (MW > 0) {
       const u32x4* p = reinterpret_cast<const u32x4*>(row);

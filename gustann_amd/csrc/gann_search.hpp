@@ -59,6 +59,22 @@ struct RecRegs {
       x[k] = i < ix.dim ? xs[i] : T(0);
     }
   }
+  // load() with every lane loading, at clamped addresses: a fixed number of
+  // loads whatever the lane mask, so a later wait can count the loads issued
+  // after them exactly.  Neighbours past R and coordinates past dim hold
+  // copies of the last ones; every use is under lane < deg <= R or i < dim.
+  __device__ __forceinline__ void load_fixed(const IndexDev& ix, int64_t u) {
+    const uint8_t* rec = record_of(ix, u);
+    const int lane = lane_id();
+    deg_raw = *reinterpret_cast<const int32_t*>(rec + ix.data_len);
+    const uint32_t* edge = reinterpret_cast<const uint32_t*>(rec + ix.data_len + 4);
+#pragma unroll
+    for (int b = 0; b < kNB; ++b) v[b] = edge[min(lane + kWave * b, ix.R - 1)];
+    xs = reinterpret_cast<const T*>(rec);
+    const int l = lane & 31;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) x[k] = xs[min(l + 32 * k, ix.dim - 1)];
+  }
   // square_sum_32 (src/impl/util.cuh:26-46): lane l's partial over dims l,
   // l+32, ... in ascending order (registers first, then the record for dims
   // from 32 kPer, with the query restored from q and the centroid as
@@ -320,20 +336,18 @@ __device__ __forceinline__ PV lds_at(uint32_t a) {
   return *reinterpret_cast<const __attribute__((address_space(3))) PV*>((size_t)a);
 }
 
-// kWide (pivot table read through the caches, none of it in LDS): the
-// pivot rows of all 16 MW chunks are requested before the first is used, so
-// a lookup waits for one cache round trip instead of one per 8 chunks; the
-// 64 MW W-float rows need the register budget of 8-wave workgroups.
-template <int W, int MW, int kSplitG = 0, bool kPivLds = false, bool kSplitLds = false, bool kWide = false>
-__device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uint32_t rowb,
-                                        const PQDev& pq, const CodeRow<MW>& row,
-                                        const uint8_t* crow, const uint8_t* pivl = nullptr) {
-  float dist = 0.0f;
-  if constexpr (kWide) {
-    static_assert(MW > 0 && (W == 4 || W == 2) && kSplitG == 0 && !kPivLds, "wide form: whole table in HBM");
-    typedef typename PivotVec<W>::type PV;
-    constexpr int kM = 16 * MW;
-    PV p[kM];
+// The wide lookup in two steps: issue() requests the pivot rows of all 16 MW
+// chunks of a code row (`piv` in HBM, `rowb` bytes per row), sum() adds the
+// chunk distances in order 0 .. M-1 (the LUT's arithmetic, src/impl/pq.cuh:
+// 35-43, and the ADC's order, src/impl/pure_mem.cuh:306-308).  Loads the
+// caller issues between the two do not delay the rows sum() waits for.
+template <int MW, int W>
+struct WidePivots {
+  static_assert(MW > 0 && (W == 4 || W == 2), "16 MW chunks of 2 or 4 dims");
+  typedef typename PivotVec<W>::type PV;
+  static constexpr int kM = 16 * MW;
+  PV p[kM];
+  __device__ __forceinline__ void issue(const uint8_t* piv, uint32_t rowb, const CodeRow<MW>& row) {
 #pragma unroll
     for (int k = 0; k < MW; ++k) {
       const uint32_t ws[4] = {row.w[k].x, row.w[k].y, row.w[k].z, row.w[k].w};
@@ -343,6 +357,9 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
         p[16 * k + b] = *reinterpret_cast<const PV*>(piv + cb_row(c, rowb) + (16 * k + b) * W * 4);
       }
     }
+  }
+  __device__ __forceinline__ float sum(const float* qs) const {
+    float dist = 0.0f;
 #pragma unroll
     for (int g = 0; g < kM / 8; ++g) {
       uint64_t qa = (uint64_t)(qs + 8 * g * W);
@@ -359,6 +376,24 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
         dist = dist + cb_chunk<W>(qv + b * W, pv);
       }
     }
+    return dist;
+  }
+};
+
+// kWide (pivot table read through the caches, none of it in LDS): the
+// pivot rows of all 16 MW chunks are requested before the first is used, so
+// a lookup waits for one cache round trip instead of one per 8 chunks; the
+// 64 MW W-float rows need the register budget of 8-wave workgroups.
+template <int W, int MW, int kSplitG = 0, bool kPivLds = false, bool kSplitLds = false, bool kWide = false>
+__device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uint32_t rowb,
+                                        const PQDev& pq, const CodeRow<MW>& row,
+                                        const uint8_t* crow, const uint8_t* pivl = nullptr) {
+  float dist = 0.0f;
+  if constexpr (kWide) {
+    static_assert(kSplitG == 0 && !kPivLds, "wide form: whole table in HBM");
+    WidePivots<MW, W> wp;
+    wp.issue(piv, rowb, row);
+    dist = wp.sum(qs);
   } else if constexpr (MW > 0 && (W == 4 || W == 2)) {
     typedef typename PivotVec<W>::type PV;
 #pragma unroll
@@ -487,13 +522,53 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
     int sz = 0, fu = 0;
     TopK top(td, ti, topk);
     int32_t exps = 0, adcs = 0;
+    // kSpec (the wide form, one neighbour block): the node after next is
+    // guessed as the first unvisited entry once the list is updated (right
+    // unless next's expansion inserts before it), and its record is
+    // requested right after the next expansion's pivot reads, its code rows
+    // right after that expansion's ADC.  A right guess finds record and rows
+    // in flight or in registers; a wrong one loads them as the plain loop
+    // does.  Only where data is fetched changes: every value used is the
+    // one the plain loop loads.  The guess loads come after the loads the
+    // expansion waits for, so they never hold those up.
+    constexpr bool kSpec = kSplitG == kGpWide && NB == 1;
+    CodeRow<MW> rows;       // cur's code rows (lanes past deg: all codes 0)
+    bool rows_ok = false;   // rows already requested for cur (uniform)
+    RecRegs<T, KP, NB> gs;  // the guessed next node's record
+    CodeRow<MW> grows;      // and its code rows
+    int32_t g_id = -1;      // the guess (-1: none)
     while (u >= 0 && exps < cap) {
       ++exps;
       const int deg = __builtin_amdgcn_readfirstlane(min(max(cur.deg_raw, 0), R));
       adcs += deg;
       uint64_t key[NB];
+      if constexpr (kSpec) {
+        if (!rows_ok) {
+          if (lane < deg)
+            rows.load(pq.codes + (int64_t)cur.v[0] * M, M);
+          else
+            rows.zero();
+        }
+        WidePivots<MW, W> wp;
+        wp.issue(piv, rowb, rows);
+        // the fences keep this order: pivot reads, guess record, the sum
+        // (waiting for the pivot reads only), then the first use of the
+        // guess record
+        asm volatile("" ::: "memory");
+        gs.load_fixed(ix, g_id >= 0 ? g_id : 0);
+        float d = wp.sum(qs);
+        asm volatile("" : "+v"(d));
+        asm volatile("" : "+v"(gs.deg_raw));
+        key[0] = lane < deg ? make_key(d, cur.v[0]) : ~(uint64_t)0;
+        const int gdeg = __builtin_amdgcn_readfirstlane(min(max(gs.deg_raw, 0), R));
+        if (lane < gdeg)
+          grows.load(pq.codes + (int64_t)gs.v[0] * M, M);
+        else
+          grows.zero();
+      }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
+        if constexpr (kSpec) break;
         key[b] = ~(uint64_t)0;  // padding sorts last
         if (lane + kWave * b < deg) {
           CodeRow<MW> row;
@@ -509,12 +584,22 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
       const int32_t next =
           __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)entry_id(P.sel) : -1);
       RecRegs<T, KP, NB> nxt;
-      if (next >= 0) nxt.load(ix, next);
+      bool nrows_ok = false;
+      if (kSpec && next >= 0 && next == g_id) {
+        nxt = gs;
+        rows = grows;
+        nrows_ok = true;
+      } else if (next >= 0) {
+        nxt.load(ix, next);
+      }
       fu = list_apply(A, BM, P);
       sz = P.nsz;
       top.push(du, u);
+      if constexpr (kSpec)
+        g_id = next >= 0 && fu < sz ? __builtin_amdgcn_readfirstlane((int32_t)entry_id(A[fu])) : -1;
       u = next;
       cur = nxt;
+      rows_ok = nrows_ok;
     }
     top.store(nns, dists, qi);
     if (lane == 0) {
