@@ -49,8 +49,11 @@ __host__ __device__ constexpr int list_capacity(int L) { return (L + kWave - 1) 
 // below it.  A first level shared by all lanes splits the list into 9
 // segments of s entries and reads the last entry of the first 8 (uniform
 // addresses); the entries below key are a prefix of those probes, so their
-// count fixes the lane's segment, which a branchless binary search with
-// uniform steps finishes.
+// count fixes the lane's segment.  Uniform steps finish it: one binary step
+// when the largest power of two q within the span is an odd power, then
+// 4-ary levels q, q/4, ..., 1 of 3 probes each, issued together (reads
+// clamped into the segment, probes at or past its end count as not below),
+// so a 263-entry segment takes 5 dependent LDS reads instead of 9.
 __device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key, bool active) {
   if (!active) return 0;
   int lo = 0, end = sz, span = sz;  // answer in [lo, end]; span bounds end - lo
@@ -63,9 +66,21 @@ __device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key
     end = cnt == 8 ? sz : min(s * (cnt + 1) - 1, sz - 1);
     span = s;
   }
-  for (int step = span > 0 ? 1 << (31 - __builtin_clz((unsigned)span)) : 0; step > 0; step >>= 1) {
-    const int p = lo + step - 1;
-    if (p < end && A[p] < key) lo += step;
+  if (span <= 0) return lo;
+  const int last = max(end - 1, 0);
+  int lq = 31 - __builtin_clz((unsigned)span);  // q = 1 << lq, uniform
+  if (lq & 1) {
+    const int p = lo + (1 << lq) - 1;
+    const uint64_t a = A[min(p, last)];
+    if (p < end && a < key) lo += 1 << lq;
+    --lq;
+  }
+  for (; lq >= 0; lq -= 2) {
+    const int q = 1 << lq;
+    const int p1 = lo + q - 1, p2 = p1 + q, p3 = p2 + q;
+    const uint64_t a1 = A[min(p1, last)], a2 = A[min(p2, last)], a3 = A[min(p3, last)];
+    const int c = (p1 < end && a1 < key ? 1 : 0) + (p2 < end && a2 < key ? 1 : 0) + (p3 < end && a3 < key ? 1 : 0);
+    lo += c * q;
   }
   return lo;
 }

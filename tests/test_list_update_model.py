@@ -137,3 +137,52 @@ def test_duplicate_of_the_last_entry_is_dropped():
         new, _, n, _ = device_update(cur, [key_of(L - 1, 10 + L - 1)], L, 0)
         assert n == 0 and new == cur
         assert reference_update(cur, [key_of(L - 1, 10 + L - 1)], L) == cur
+
+
+def device_rank(A, sz, key):
+    """list_rank's index arithmetic (gann_list.hpp): a uniform first level of
+    8 probes splitting A[0..sz) into 9 segments, then uniform steps inside
+    the segment -- one binary step when the largest power of two within the
+    segment's span is an odd power, then 4-ary levels of 3 probes (reads
+    clamped to the segment's end, probes at or past it count as not below)."""
+    lo, end, span = 0, sz, sz
+    if sz > 8:
+        s = (sz + 8) // 9
+        cnt = sum(1 for m in range(8) if A[min(s * (m + 1) - 1, sz - 1)] < key)
+        lo = min(s * cnt, sz)
+        end = sz if cnt == 8 else min(s * (cnt + 1) - 1, sz - 1)
+        span = s
+    q = 1 << (span.bit_length() - 1) if span > 0 else 0
+    reads = 0
+    if q > 0 and (q.bit_length() - 1) & 1:
+        p = lo + q - 1
+        if p < end and A[min(p, max(end - 1, 0))] < key:
+            lo += q
+        reads += 1
+        q >>= 1
+    while q > 0:
+        c = 0
+        for j in (1, 2, 3):
+            p = lo + j * q - 1
+            c += 1 if (p < end and A[min(p, max(end - 1, 0))] < key) else 0
+            reads += 1
+        lo += c * q
+        q >>= 2
+    return lo, reads
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_device_rank_is_lower_bound(seed):
+    # every size class of the first level and of the uniform steps, keys
+    # below, between, equal to and above the entries
+    rng = random.Random(seed)
+    sizes = list(range(0, 70)) + [rng.randrange(70, 3000) for _ in range(60)] + [2575, 2576, 2624, 4096]
+    for sz in sizes:
+        A = sorted(rng.sample(range(0, 1 << 40, 2), sz))
+        probes = [0, (1 << 40) + 1] + [rng.randrange(0, 1 << 40) for _ in range(20)]
+        probes += [a for a in rng.sample(A, min(sz, 10))] + [a + 1 for a in rng.sample(A, min(sz, 10))]
+        for key in probes:
+            r, reads = device_rank(A, sz, key)
+            assert r == bisect.bisect_left(A, key), (sz, key)
+            if sz > 8:
+                assert reads <= 16
