@@ -181,7 +181,6 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
     // inserted entries placed below the end of the current chunk, counted
     // down from the top chunk
     int below = __popcll(ballot64(placed));
-    const uint64_t lanebit = 1ull << lane;
     wave_sync();
     for (int b_hi = nch; b_hi > 0; b_hi -= kBatch) {
       const int b_lo = max(0, b_hi - kBatch);
@@ -202,9 +201,13 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
                             (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw);
         if (!rep) below -= __popcll(mo) - (c == nch - 1 ? n_tail : 0);  // now: placed below the chunk
         const int j = ob_lo + kWave * c + lane;
-        const int nb = below + rank_below(mo);
+        // nb = below + marked positions of the chunk below this lane (the
+        // count folded into mbcnt's addend); a marked lane keeps its entry,
+        // selected by the mask itself (one v_cndmask)
+        const int nb = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mo >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mo, (uint32_t)below));
         dst[t] = j;
-        val[t] = A[(mo & lanebit) ? j : j - nb];
+        val[t] = A[(int)lane_select(mo, (uint32_t)(j - nb), (uint32_t)j)];
       }
       wave_sync();
 #pragma unroll
