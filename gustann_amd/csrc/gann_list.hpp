@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include <climits>
+#include <type_traits>
 
 #include "gann_device.hpp"
 
@@ -153,8 +154,8 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
 // positions the inserted entries take are marked in the bitmap BM; output
 // position j then holds inserted entry nb(j) (nb = inserted entries placed
 // before j) if marked, else old entry j - nb(j).  The old entries are
-// gathered into the unmarked positions in batches of 16 chunks, top batch
-// first: a batch reads only positions below its highest output and at or
+// gathered into the unmarked positions in batches of 16 chunks (the last one
+// 8 or 4), top batch first: a batch reads only positions below its highest output and at or
 // above its lowest output minus 64, and writes after all its reads, so no
 // source is overwritten before it is read; then each inserted entry is stored
 // at its marked position by the lane that holds it.
@@ -182,18 +183,20 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
     // down from the top chunk
     int below = __popcll(ballot64(placed));
     wave_sync();
-    for (int b_hi = nch; b_hi > 0; b_hi -= kBatch) {
-      const int b_lo = max(0, b_hi - kBatch);
+    // straight-line batches: every lane reads one entry per chunk and writes
+    // it back, with no branch between the reads and the writes (a lane whose
+    // output does not move -- a marked position -- rewrites its own entry);
+    // slots past the bottom of a batch repeat its bottom chunk, the same
+    // reads and writes twice.  16-chunk batches from the top, the rest in
+    // one batch of 8 or 4 chunks, so at most 7 slots repeat.
+    auto batch = [&](auto kb, int b_hi) {
+      constexpr int kB = decltype(kb)::value;
+      const int b_lo = max(0, b_hi - kB);
       const uint32_t wv = lane < 2 * (b_hi - b_lo) ? BM[w_lo + 2 * b_lo + lane] : 0u;
-      // straight-line: every lane reads one entry and writes one back, with
-      // no branch between the reads and the writes (a lane whose output does
-      // not move -- a marked position -- rewrites its own entry; slots past
-      // the bottom of the batch repeat its bottom chunk, the same reads and
-      // writes twice)
-      uint64_t val[kBatch];
-      int dst[kBatch];
+      uint64_t val[kB];
+      int dst[kB];
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
+      for (int t = 0; t < kB; ++t) {
         const bool rep = b_hi - 1 - t < b_lo;              // uniform
         const int c = rep ? b_lo : b_hi - 1 - t;           // chunk, top first
         const int tw = c - b_lo;
@@ -211,9 +214,16 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
       }
       wave_sync();
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) A[dst[t]] = val[t];
+      for (int t = 0; t < kB; ++t) A[dst[t]] = val[t];
       wave_sync();
-    }
+      return b_lo;
+    };
+    int b_hi = nch;
+    while (b_hi > 8) b_hi = batch(std::integral_constant<int, kBatch>{}, b_hi);
+    if (b_hi > 4)
+      b_hi = batch(std::integral_constant<int, 8>{}, b_hi);
+    else if (b_hi > 0)
+      b_hi = batch(std::integral_constant<int, 4>{}, b_hi);
     // the inserted entries into their marked positions, after every old
     // entry has moved out of the way
     if (placed) A[P.p] = P.nkey;
