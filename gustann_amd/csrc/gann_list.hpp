@@ -155,7 +155,7 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
 // position j then holds inserted entry nb(j) (nb = inserted entries placed
 // before j) if marked, else old entry j - nb(j).  The old entries are
 // gathered into the unmarked positions in batches of 16 chunks (the last one
-// 8 or 4), top batch first: a batch reads only positions below its highest output and at or
+// 8, 4, 2 or 1), top batch first: a batch reads only positions below its highest output and at or
 // above its lowest output minus 64, and writes after all its reads, so no
 // source is overwritten before it is read; then each inserted entry is stored
 // at its marked position by the lane that holds it.
@@ -188,7 +188,7 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
     // output does not move -- a marked position -- rewrites its own entry);
     // slots past the bottom of a batch repeat its bottom chunk, the same
     // reads and writes twice.  16-chunk batches from the top, the rest in
-    // one batch of 8 or 4 chunks, so at most 7 slots repeat.
+    // one batch of 8, 4, 2 or 1 chunks, so at most 7 slots repeat.
     auto batch = [&](auto kb, int b_hi) {
       constexpr int kB = decltype(kb)::value;
       const int b_lo = max(0, b_hi - kB);
@@ -222,8 +222,12 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
     while (b_hi > 8) b_hi = batch(std::integral_constant<int, kBatch>{}, b_hi);
     if (b_hi > 4)
       b_hi = batch(std::integral_constant<int, 8>{}, b_hi);
-    else if (b_hi > 0)
+    else if (b_hi > 2)
       b_hi = batch(std::integral_constant<int, 4>{}, b_hi);
+    else if (b_hi > 1)
+      b_hi = batch(std::integral_constant<int, 2>{}, b_hi);
+    else if (b_hi > 0)
+      b_hi = batch(std::integral_constant<int, 1>{}, b_hi);
     // the inserted entries into their marked positions, after every old
     // entry has moved out of the way
     if (placed) A[P.p] = P.nkey;
