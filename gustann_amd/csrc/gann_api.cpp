@@ -841,7 +841,12 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
         gp = true;
       }
     }
-    const int waves = gp ? gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, true, g) : w_lds;
+    int waves = gp ? gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, true, g) : w_lds;
+    // tuning override: GANN_CB_WAVES=n caps the lists (waves) per CU
+    if (const char* e = std::getenv("GANN_CB_WAVES")) {
+      const int cap = std::atoi(e);
+      if (cap >= 1) waves = std::min(waves, cap);
+    }
     if (waves >= 1 && (gp || waves >= 2)) {
       int32_t* ctr = sc.counters();
       float* qs = sc.qs((int64_t)nq * Ly.dim);

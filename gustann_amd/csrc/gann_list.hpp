@@ -52,11 +52,18 @@ __host__ __device__ constexpr int list_capacity(int L) { return (L + kWave - 1) 
 // addresses); the entries below key are a prefix of those probes, so their
 // count fixes the lane's segment.  Uniform steps finish it: one binary step
 // when the largest power of two q within the span is an odd power, then
-// 4-ary levels q, q/4, ..., 1 of 3 probes each, issued together (reads
+// 4-ary levels q, q/4, ..., 4 of 3 probes each, issued together (reads
 // clamped into the segment, probes at or past its end count as not below),
-// so a 263-entry segment takes 5 dependent LDS reads instead of 9.
-__device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key, bool active) {
-  if (!active) return 0;
+// then the level q = 1, which reads the four entries from its lower bound
+// so that the entry at the result arrives with it (at_r: the entry at
+// min(result, sz - 1), for the duplicate test).  A 263-entry segment takes 5
+// dependent LDS reads instead of 9 plus the duplicate test's.  Every lane
+// runs the search, whether its key is live or not (`active`: the result is
+// 0 where it is not), so that the first level's reads, at addresses the same
+// in every lane, are issued together rather than one after another under
+// the live lanes' mask.
+__device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key, bool active, uint64_t& at_r) {
+  at_r = 0;
   int lo = 0, end = sz, span = sz;  // answer in [lo, end]; span bounds end - lo
   if (sz > 8) {
     const int s = (sz + 8) / 9;
@@ -67,8 +74,8 @@ __device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key
     end = cnt == 8 ? sz : min(s * (cnt + 1) - 1, sz - 1);
     span = s;
   }
-  if (span <= 0) return lo;
-  const int last = max(end - 1, 0);
+  if (span <= 0) return 0;  // sz == 0
+  const int last = max(end - 1, 0), top = sz - 1;
   int lq = 31 - __builtin_clz((unsigned)span);  // q = 1 << lq, uniform
   if (lq & 1) {
     const int p = lo + (1 << lq) - 1;
@@ -76,14 +83,22 @@ __device__ __forceinline__ int list_rank(const uint64_t* A, int sz, uint64_t key
     if (p < end && a < key) lo += 1 << lq;
     --lq;
   }
-  for (; lq >= 0; lq -= 2) {
+  for (; lq >= 2; lq -= 2) {
     const int q = 1 << lq;
     const int p1 = lo + q - 1, p2 = p1 + q, p3 = p2 + q;
     const uint64_t a1 = A[min(p1, last)], a2 = A[min(p2, last)], a3 = A[min(p3, last)];
     const int c = (p1 < end && a1 < key ? 1 : 0) + (p2 < end && a2 < key ? 1 : 0) + (p3 < end && a3 < key ? 1 : 0);
     lo += c * q;
   }
-  return lo;
+  // q = 1: positions lo .. lo + 2 decide, lo + 3 is read for at_r only;
+  // clamping to sz - 1 instead of the segment's end reads the same entries
+  // wherever a probe counts (below end <= sz)
+  const uint64_t a0 = A[min(lo, top)], a1 = A[min(lo + 1, top)], a2 = A[min(lo + 2, top)],
+                 a3 = A[min(lo + 3, top)];
+  const int c = (lo < end && a0 < key ? 1 : 0) + (lo + 1 < end && a1 < key ? 1 : 0) +
+                (lo + 2 < end && a2 < key ? 1 : 0);
+  at_r = c == 0 ? a0 : c == 1 ? a1 : c == 2 ? a2 : a3;
+  return active ? lo + c : 0;
 }
 
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
@@ -118,9 +133,10 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
   const int lane = lane_id();
   const uint64_t fu_entry = fu < sz ? A[fu] : 0;
   const bool active = lane < deg;
-  uint32_t r = (uint32_t)list_rank(A, sz, key, active);
+  uint64_t at_r;
+  uint32_t r = (uint32_t)list_rank(A, sz, key, active, at_r);
   // a candidate whose id is listed already sits at its lower bound
-  const bool dup = active && (int)r < sz && entry_id(A[r]) == entry_id(key);
+  const bool dup = active && (int)r < sz && entry_id(at_r) == entry_id(key);
   if (!active || dup || (int)r >= L) key = ~(uint64_t)0;  // never a real key: ids are < 2^31 - 1
   const uint64_t live = ballot64(key != ~(uint64_t)0);
   // uniform branches; the sort keeps the count

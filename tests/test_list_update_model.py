@@ -143,8 +143,11 @@ def device_rank(A, sz, key):
     """list_rank's index arithmetic (gann_list.hpp): a uniform first level of
     8 probes splitting A[0..sz) into 9 segments, then uniform steps inside
     the segment -- one binary step when the largest power of two within the
-    segment's span is an odd power, then 4-ary levels of 3 probes (reads
-    clamped to the segment's end, probes at or past it count as not below)."""
+    segment's span is an odd power, 4-ary levels of 3 probes (reads clamped
+    to the segment's end, probes at or past it count as not below) down to
+    q = 4, and the level q = 1, which reads four entries from its lower bound
+    clamped to sz - 1 and returns the one at the result.  Returns (rank,
+    entry at min(rank, sz - 1) or None, reads after the first level)."""
     lo, end, span = 0, sz, sz
     if sz > 8:
         s = (sz + 8) // 9
@@ -152,23 +155,30 @@ def device_rank(A, sz, key):
         lo = min(s * cnt, sz)
         end = sz if cnt == 8 else min(s * (cnt + 1) - 1, sz - 1)
         span = s
-    q = 1 << (span.bit_length() - 1) if span > 0 else 0
+    if span <= 0:
+        return 0, None, 0
+    last, top = max(end - 1, 0), sz - 1
+    lq = span.bit_length() - 1
     reads = 0
-    if q > 0 and (q.bit_length() - 1) & 1:
-        p = lo + q - 1
-        if p < end and A[min(p, max(end - 1, 0))] < key:
-            lo += q
+    if lq & 1:
+        p = lo + (1 << lq) - 1
+        if p < end and A[min(p, last)] < key:
+            lo += 1 << lq
         reads += 1
-        q >>= 1
-    while q > 0:
+        lq -= 1
+    while lq >= 2:
+        q = 1 << lq
         c = 0
         for j in (1, 2, 3):
             p = lo + j * q - 1
-            c += 1 if (p < end and A[min(p, max(end - 1, 0))] < key) else 0
+            c += 1 if (p < end and A[min(p, last)] < key) else 0
             reads += 1
         lo += c * q
-        q >>= 2
-    return lo, reads
+        lq -= 2
+    vals = [A[min(lo + j, top)] for j in range(4)]
+    reads += 4
+    c = sum(1 for j in range(3) if lo + j < end and vals[j] < key)
+    return lo + c, vals[c], reads
 
 
 @pytest.mark.parametrize("seed", range(6))
@@ -182,7 +192,9 @@ def test_device_rank_is_lower_bound(seed):
         probes = [0, (1 << 40) + 1] + [rng.randrange(0, 1 << 40) for _ in range(20)]
         probes += [a for a in rng.sample(A, min(sz, 10))] + [a + 1 for a in rng.sample(A, min(sz, 10))]
         for key in probes:
-            r, reads = device_rank(A, sz, key)
+            r, at_r, reads = device_rank(A, sz, key)
             assert r == bisect.bisect_left(A, key), (sz, key)
+            if sz > 0:
+                assert at_r == A[min(r, sz - 1)], (sz, key)
             if sz > 8:
                 assert reads <= 16
