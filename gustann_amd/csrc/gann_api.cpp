@@ -847,6 +847,13 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
       const int cap = std::atoi(e);
       if (cap >= 1) waves = std::min(waves, cap);
     }
+    // the wide form keeps its first chunks in the LDS the lists leave, up to
+    // gann::kCbMaxWideLds of them (GANN_WIDE_LDS=n caps that, 0: none)
+    if (gp && g == gann::kCbGpWide && waves >= 1) {
+      int nl = gann::search_cb_wide_lds_chunks(cw, L, topk, h->lds_limit, waves, (int)h->ix.R);
+      if (const char* e = std::getenv("GANN_WIDE_LDS")) nl = std::min(nl, std::max(0, std::atoi(e)));
+      g = gann::kCbGpWide - nl;
+    }
     if (waves >= 1 && (gp || waves >= 2)) {
       int32_t* ctr = sc.counters();
       float* qs = sc.qs((int64_t)nq * Ly.dim);

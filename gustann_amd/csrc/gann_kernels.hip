@@ -366,6 +366,13 @@ int search_cb_split_groups(int M, int chunk_w) {
   return (mw_of(M) > 0 && (chunk_w == 2 || chunk_w == 4)) ? M / 8 : 0;
 }
 
+int search_cb_wide_lds_chunks(int chunk_w, int L, int topk, size_t lds_limit, int waves, int R) {
+  if (R > kWave || chunk_w <= 0) return 0;
+  const size_t used = (size_t)waves * CbSmem::wave_bytes(L, topk);
+  if (used >= lds_limit) return 0;
+  return (int)std::min<size_t>((size_t)kCbMaxWideLds, (lds_limit - used) / cb_wide_lds_bytes(1, chunk_w));
+}
+
 bool search_cb_wide_ok(int M, int chunk_w, int dim) {
   const int mw = mw_of(M);
   return mw > 0 && (chunk_w == 2 || chunk_w == 4) && 16 * mw * chunk_w <= 128 && dim == M * chunk_w;
@@ -402,12 +409,14 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
                             hipStream_t stream) {
   if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
   const int split = search_cb_split_groups(pq.M, pq.chunk_w);
-  if (lds_groups == kCbGpWide) {
+  if (cb_is_wide(lds_groups)) {
     if (!global_pivots || !search_cb_wide_ok(pq.M, pq.chunk_w, ix.dim)) return hipErrorInvalidValue;
+    if (cb_wide_lds(lds_groups) > 0 && ix.R > kWave) return hipErrorInvalidValue;
   } else if (lds_groups != 0 && (!global_pivots || (lds_groups != split - 1 && lds_groups != split / 2))) {
     return hipErrorInvalidValue;
   }
   const size_t smem = (global_pivots ? split_pivot_bytes(lds_groups, pq.chunk_w) : CbSmem::pivot_bytes(ix.dim)) +
+                      cb_wide_lds_bytes(cb_wide_lds(lds_groups), pq.chunk_w) +
                       (size_t)waves * CbSmem::wave_bytes(L, topk);
   hipError_t e = prepare_cb(ix, pq, q, nq, queue, qs_all, stream);
   if (e != hipSuccess) return e;

@@ -45,6 +45,22 @@ int search_cb_split_groups(int M, int chunk_w);
 // (16, 32 or 64 chunks of 2 or 4 dims, at most 128 dims).
 constexpr int kCbGpWide = -1;
 bool search_cb_wide_ok(int M, int chunk_w, int dim);
+// The wide form can also keep its first G chunks (1 <= G <= kCbMaxWideLds,
+// graph degree <= 64) in a partial pivot table in LDS, in the LDS the lists
+// leave: lds_groups = kCbGpWide - G.
+constexpr int kCbMaxWideLds = 3;
+__host__ __device__ constexpr bool cb_is_wide(int lds_groups) {
+  return lds_groups <= kCbGpWide && lds_groups >= kCbGpWide - kCbMaxWideLds;
+}
+__host__ __device__ constexpr int cb_wide_lds(int lds_groups) {
+  return cb_is_wide(lds_groups) ? kCbGpWide - lds_groups : 0;
+}
+// LDS bytes of the wide form's partial table of G chunks of chunk_w dims.
+__host__ __device__ constexpr size_t cb_wide_lds_bytes(int G, int chunk_w) {
+  return (size_t)256 * G * chunk_w * 4;
+}
+// The most chunks (<= kCbMaxWideLds) that fit beside `waves` lists.
+int search_cb_wide_lds_chunks(int chunk_w, int L, int topk, size_t lds_limit, int waves, int R);
 // Size and contents of pq.piv_cb: the pivots [256][dim] in the kernel's row layout.
 size_t search_cb_pivot_bytes(int dim);
 void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out);

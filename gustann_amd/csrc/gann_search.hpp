@@ -341,7 +341,9 @@ __device__ __forceinline__ PV lds_at(uint32_t a) {
 // chunk distances in order 0 .. M-1 (the LUT's arithmetic, src/impl/pq.cuh:
 // 35-43, and the ADC's order, src/impl/pure_mem.cuh:306-308).  Loads the
 // caller issues between the two do not delay the rows sum() waits for.
-template <int MW, int W>
+// kWL > 0: the first kWL chunks come from a partial table at LDS address 0
+// (rows of kWL * W floats, no padding), the others from piv.
+template <int MW, int W, int kWL = 0>
 struct WidePivots {
   static_assert(MW > 0 && (W == 4 || W == 2), "16 MW chunks of 2 or 4 dims");
   typedef typename PivotVec<W>::type PV;
@@ -354,7 +356,11 @@ struct WidePivots {
 #pragma unroll
       for (int b = 0; b < 16; ++b) {
         const uint32_t c = (ws[b >> 2] >> (8 * (b & 3))) & 0xffu;
-        p[16 * k + b] = *reinterpret_cast<const PV*>(piv + cb_row(c, rowb) + (16 * k + b) * W * 4);
+        const int j = 16 * k + b;
+        if (j < kWL)  // compile-time
+          p[j] = lds_at<PV>(cb_row(c, kWL * W * 4) + j * W * 4);
+        else
+          p[j] = *reinterpret_cast<const PV*>(piv + cb_row(c, rowb) + j * W * 4);
       }
     }
   }
@@ -453,14 +459,16 @@ constexpr int kGpWide = kCbGpWide;
 // (kGpWide) in flight (the 128-VGPR cap of 16-wave workgroups would spill
 // them).
 __host__ __device__ constexpr int cb_block_threads(int KP, int kSplitG = 0) {
-  return (KP > 8 || kSplitG == kGpWide) ? 512 : 1024;
+  return (KP > 8 || cb_is_wide(kSplitG)) ? 512 : 1024;
 }
 
 // kGP: the pivot table is read from pq.piv_cb (HBM, through the caches)
 // instead of a copy in LDS, which then holds only the per-wave lists: the
 // form for large L, where lists beside a 128 KB table leave few waves.
 // kSplitG > 0 (with kGP): that many groups of 8 chunks also in LDS;
-// kSplitG == kGpWide (with kGP): the wide lookup of cb_adc, 8-wave
+// kSplitG == kGpWide - G (with kGP): the wide lookup of cb_adc, 8-wave
+// workgroups, the first G chunks (one neighbour block only) from a partial
+// table in LDS;
 // workgroups.  KP: rerank coordinates per lane held in registers; NB:
 // neighbour blocks.
 template <typename T, int MW, int W, bool kGP, int kSplitG, int KP, int NB>
@@ -474,8 +482,20 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
   const uint32_t rowb = cb_stride(4 * dim);
   const uint8_t* piv;
   size_t lists_at = 0;
+  constexpr int kWL = cb_wide_lds(kSplitG);
+  static_assert(kWL == 0 || NB == 1, "the wide form's LDS chunks serve one neighbour block");
   if constexpr (kGP) {
     piv = (const uint8_t*)((const __attribute__((address_space(1))) uint8_t*)pq.piv_cb);
+    if constexpr (kWL > 0) {
+      // the first kWL chunks (dims 0 .. kWL W - 1) at LDS address 0
+      constexpr int per_row = kWL * W;
+      for (int idx = threadIdx.x; idx < kPivots * per_row; idx += blockDim.x) {
+        const int c = idx / per_row, i = idx - c * per_row;
+        *reinterpret_cast<float*>(smem_raw + 4 * idx) = pq.pivots[c * dim + i];
+      }
+      __syncthreads();
+      lists_at = cb_wide_lds_bytes(kWL, W);
+    }
     if constexpr (kSplitG > 0) {
       // the first kSplitG groups of 8 chunks also in LDS
       constexpr int per_row = kSplitG * 8 * W;
@@ -531,7 +551,7 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
     // does.  Only where data is fetched changes: every value used is the
     // one the plain loop loads.  The guess loads come after the loads the
     // expansion waits for, so they never hold those up.
-    constexpr bool kSpec = kSplitG == kGpWide && NB == 1;
+    constexpr bool kSpec = cb_is_wide(kSplitG) && NB == 1;
     CodeRow<MW> rows;       // cur's code rows (lanes past deg: all codes 0)
     bool rows_ok = false;   // rows already requested for cur (uniform)
     RecRegs<T, KP, NB> gs;  // the guessed next node's record
@@ -549,7 +569,7 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
           else
             rows.zero();
         }
-        WidePivots<MW, W> wp;
+        WidePivots<MW, W, kWL> wp;
         wp.issue(piv, rowb, rows);
         // the fences keep this order: pivot reads, guess record, the sum
         // (waiting for the pivot reads only), then the first use of the
@@ -574,7 +594,7 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
           CodeRow<MW> row;
           const uint8_t* crow = pq.codes + (int64_t)cur.v[b] * M;
           row.load(crow, M);
-          key[b] = make_key(cb_adc<W, MW, (kSplitG > 0 ? kSplitG : 0), !kGP, (KP <= 4), (kSplitG == kGpWide)>(
+          key[b] = make_key(cb_adc<W, MW, (kSplitG > 0 ? kSplitG : 0), !kGP, (KP <= 4), cb_is_wide(kSplitG)>(
                                 piv, qs, rowb, pq, row, crow, smem_raw),
                             cur.v[b]);
         }
@@ -920,7 +940,7 @@ hipError_t launch_search_cb_t(const IndexDev& ix, const PQDev& pq, const float* 
     constexpr int NBv = decltype(nb)::value;
     return with_cb_shape(pq.M, pq.chunk_w, ix.dim, [&](auto mw, auto w, auto kp) {
       constexpr int MWv = decltype(mw)::value, Wv = decltype(w)::value, KPv = decltype(kp)::value;
-      if (waves * kWave > cb_block_threads(KPv, lds_groups == kGpWide ? kGpWide : 0))
+      if (waves * kWave > cb_block_threads(KPv, cb_is_wide(lds_groups) ? kGpWide : 0))
         return hipErrorInvalidConfiguration;
       // the split forms keep part of the table in LDS for one neighbour
       // block; with two the extra live registers would spill
@@ -930,11 +950,23 @@ hipError_t launch_search_cb_t(const IndexDev& ix, const PQDev& pq, const float* 
       // the wide form: all 16 MW pivot rows of a lookup in at most 128 registers
       constexpr bool kCanWide = MWv > 0 && 16 * MWv * Wv <= 128;
       if constexpr (kCanWide) {
-        if (global_pivots && lds_groups == kGpWide)
-          return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kGpWide, KPv, NBv>, [&] {
-            hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kGpWide, KPv, NBv>), grid, block, smem, stream,
-                               ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
-          });
+        if (global_pivots && cb_is_wide(lds_groups)) {
+          auto wide = [&](auto g) {
+            constexpr int kG = decltype(g)::value;
+            return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kG, KPv, NBv>, [&] {
+              hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kG, KPv, NBv>), grid, block, smem, stream,
+                                 ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+            });
+          };
+          if (lds_groups == kGpWide) return wide(ic<kGpWide>{});
+          if constexpr (NBv == 1) {
+            static_assert(kCbMaxWideLds == 3, "one instantiation per partial-table size");
+            if (lds_groups == kGpWide - 1) return wide(ic<kGpWide - 1>{});
+            if (lds_groups == kGpWide - 2) return wide(ic<kGpWide - 2>{});
+            if (lds_groups == kGpWide - 3) return wide(ic<kGpWide - 3>{});
+          }
+          return hipErrorInvalidValue;
+        }
       }
       if constexpr (kCanSplit) {
         if (global_pivots && lds_groups > 0 && lds_groups == kSplit)

@@ -322,9 +322,14 @@ def test_wide_lookup_form_matches_oracle(tmp_path, monkeypatch, dtype, D, M, R):
     monkeypatch.setenv("GANN_PIVOT_FORM", "wide")
     for L, topk in ((12, 5), (64, 10), (300, 100)):
         on, od, of, oe, _ = ix.search(Q, topk, L)
-        ne = np.empty(48, np.int32)
-        got = g.search(Q, 48, topk, L, n_exp=ne, mode=MODE_FUSED)
-        _assert_same(got, (on, od, of), ne, oe)
+        # the first 0, 1 or 3 chunks from a partial pivot table in LDS (one
+        # neighbour block; with two the form keeps none)
+        for wl in ("0", "1", "3"):
+            monkeypatch.setenv("GANN_WIDE_LDS", wl)
+            ne = np.empty(48, np.int32)
+            got = g.search(Q, 48, topk, L, n_exp=ne, mode=MODE_FUSED)
+            _assert_same(got, (on, od, of), ne, oe)
+    monkeypatch.delenv("GANN_WIDE_LDS", raising=False)
     monkeypatch.delenv("GANN_PIVOT_FORM", raising=False)
     g.close()
 
