@@ -170,11 +170,13 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
 // positions the inserted entries take are marked in the bitmap BM; output
 // position j then holds inserted entry nb(j) (nb = inserted entries placed
 // before j) if marked, else old entry j - nb(j).  The old entries are
-// gathered into the unmarked positions in batches of 16 chunks (the last one
-// 8, 4, 2 or 1), top batch first: a batch reads only positions below its highest output and at or
-// above its lowest output minus 64, and writes after all its reads, so no
-// source is overwritten before it is read; then each inserted entry is stored
-// at its marked position by the lane that holds it.
+// gathered into the unmarked positions in batches of 16 chunks, top batch
+// first (near the start of the list the last one may be of 8, 4, 2 or 1):
+// a batch reads only positions below its highest output and at or above its
+// lowest output minus 64, and writes after all its reads, so no source is
+// overwritten before it is read; chunks below the first insertion that a
+// batch covers have no marks and copy onto themselves.  Then each inserted
+// entry is stored at its marked position by the lane that holds it.
 // kSelect = false (beam search) only applies the insertions and returns P.lb.
 template <bool kSelect = true>
 __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListPlan& P) {
@@ -183,67 +185,97 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
   wave_sync();  // all reads of plan() done
   const int start = min(P.p0, P.nsz);
   if (start < P.nsz) {
-    const int ob_lo = (start / kWave) * kWave;
-    const int nch = (P.nsz - ob_lo + kWave - 1) / kWave;
-    const int w_lo = ob_lo / 32;
-    for (int w = lane; w < 2 * nch; w += kWave) BM[w_lo + w] = 0u;
+    const int cb = start / kWave, ct = (P.nsz - 1) / kWave;  // first and top chunk that change
+    // the last full window may sweep up to kBatch - 1 chunks below cb: their
+    // marks are cleared as well, so they copy onto themselves
+    const int c0 = max(0, cb - (kBatch - 1));
+    for (int w = lane; w < 2 * (ct - c0 + 1); w += kWave) BM[2 * c0 + w] = 0u;
     wave_sync();
     const bool placed = lane < P.n_nd && P.p < P.nsz;
     if (placed) atomicOr(&BM[P.p >> 5], 1u << (P.p & 31));
     // positions from nsz to the end of the top chunk are marked as well, so
     // that they keep their entries like the inserted positions do
-    const int jt = ob_lo + kWave * (nch - 1) + lane;
+    const int jt = kWave * ct + lane;
     if (jt >= P.nsz) atomicOr(&BM[jt >> 5], 1u << (jt & 31));
-    const int n_tail = ob_lo + kWave * nch - P.nsz;
-    // inserted entries placed below the end of the current chunk, counted
-    // down from the top chunk
-    int below = __popcll(ballot64(placed));
+    const int n_tail = kWave * (ct + 1) - P.nsz;
+    // inserted entries placed below the chunk being gathered, counted down
+    // from the top; it starts with the top chunk's n_tail extra marks, so
+    // that every chunk subtracts its whole mask
+    int below = __popcll(ballot64(placed)) + n_tail;
     wave_sync();
-    // straight-line batches: every lane reads one entry per chunk and writes
-    // it back, with no branch between the reads and the writes (a lane whose
-    // output does not move -- a marked position -- rewrites its own entry);
-    // slots past the bottom of a batch repeat its bottom chunk, the same
-    // reads and writes twice.  16-chunk batches from the top, the rest in
-    // one batch of 8, 4, 2 or 1 chunks, so at most 7 slots repeat.
-    auto batch = [&](auto kb, int b_hi) {
-      constexpr int kB = decltype(kb)::value;
-      const int b_lo = max(0, b_hi - kB);
-      const uint32_t wv = lane < 2 * (b_hi - b_lo) ? BM[w_lo + 2 * b_lo + lane] : 0u;
-      uint64_t val[kB];
-      int dst[kB];
+    // One chunk of a batch: output j = 64 c + lane takes old entry j - nb
+    // (nb = below + marked positions of the chunk below this lane, the count
+    // folded into mbcnt's addend), or keeps its own entry where it is marked
+    // (selected by the mask itself, one v_cndmask).
+    auto gather = [&](uint64_t mo, int j, uint64_t& val) {
+      const int nb = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mo >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mo, (uint32_t)below));
+      val = A[(int)lane_select(mo, (uint32_t)(j - nb), (uint32_t)j)];
+    };
+    // Straight-line batches: every lane reads one entry per chunk and writes
+    // it back, with no branch between the reads and the writes, all reads of
+    // a batch before its writes.  Full windows of kBatch chunks [b_hi - 16,
+    // b_hi) from the top: the chunk of each slot, its mask word in the batch's
+    // read and its LDS offset are fixed at compile time.
+    int b_hi = ct + 1;
+    while (b_hi > cb && b_hi >= kBatch) {
+      const int b_lo = b_hi - kBatch;
+      const uint32_t wv = lane < 2 * kBatch ? BM[2 * b_lo + lane] : 0u;
+      const int jtop = kWave * (b_hi - 1) + lane;
+      uint64_t val[kBatch];
 #pragma unroll
-      for (int t = 0; t < kB; ++t) {
-        const bool rep = b_hi - 1 - t < b_lo;              // uniform
-        const int c = rep ? b_lo : b_hi - 1 - t;           // chunk, top first
-        const int tw = c - b_lo;
-        const uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw + 1) << 32) |
-                            (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw);
-        if (!rep) below -= __popcll(mo) - (c == nch - 1 ? n_tail : 0);  // now: placed below the chunk
-        const int j = ob_lo + kWave * c + lane;
-        // nb = below + marked positions of the chunk below this lane (the
-        // count folded into mbcnt's addend); a marked lane keeps its entry,
-        // selected by the mask itself (one v_cndmask)
-        const int nb = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mo >> 32),
-                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mo, (uint32_t)below));
-        dst[t] = j;
-        val[t] = A[(int)lane_select(mo, (uint32_t)(j - nb), (uint32_t)j)];
+      for (int t = 0; t < kBatch; ++t) {
+        constexpr int kTop = 2 * (kBatch - 1);
+        const uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, kTop - 2 * t + 1) << 32) |
+                            (uint32_t)__builtin_amdgcn_readlane((int)wv, kTop - 2 * t);
+        below -= __popcll(mo);
+        gather(mo, jtop - kWave * t, val[t]);
       }
       wave_sync();
 #pragma unroll
-      for (int t = 0; t < kB; ++t) A[dst[t]] = val[t];
+      for (int t = 0; t < kBatch; ++t) A[jtop - kWave * t] = val[t];
       wave_sync();
-      return b_lo;
-    };
-    int b_hi = nch;
-    while (b_hi > 8) b_hi = batch(std::integral_constant<int, kBatch>{}, b_hi);
-    if (b_hi > 4)
-      b_hi = batch(std::integral_constant<int, 8>{}, b_hi);
-    else if (b_hi > 2)
-      b_hi = batch(std::integral_constant<int, 4>{}, b_hi);
-    else if (b_hi > 1)
-      b_hi = batch(std::integral_constant<int, 2>{}, b_hi);
-    else if (b_hi > 0)
-      b_hi = batch(std::integral_constant<int, 1>{}, b_hi);
+      b_hi = b_lo;
+    }
+    // What is left lies in the first kBatch - 1 chunks of the list: one
+    // batch of 16, 8, 4, 2 or 1 chunks [max(0, b_hi - kB), b_hi), the
+    // smallest that reaches cb; slots below chunk 0 repeat chunk 0 (the same
+    // reads and writes twice).
+    if (b_hi > cb) {
+      auto batch = [&](auto kb) {
+        constexpr int kB = decltype(kb)::value;
+        const int b_lo = max(0, b_hi - kB);
+        const uint32_t wv = lane < 2 * (b_hi - b_lo) ? BM[2 * b_lo + lane] : 0u;
+        uint64_t val[kB];
+        int dst[kB];
+#pragma unroll
+        for (int t = 0; t < kB; ++t) {
+          const bool rep = b_hi - 1 - t < b_lo;     // uniform
+          const int c = rep ? b_lo : b_hi - 1 - t;  // chunk, top first
+          const int tw = c - b_lo;
+          const uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw + 1) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw);
+          if (!rep) below -= __popcll(mo);
+          dst[t] = kWave * c + lane;
+          gather(mo, dst[t], val[t]);
+        }
+        wave_sync();
+#pragma unroll
+        for (int t = 0; t < kB; ++t) A[dst[t]] = val[t];
+        wave_sync();
+      };
+      const int r = b_hi - cb;
+      if (r > 8)
+        batch(std::integral_constant<int, kBatch>{});
+      else if (r > 4)
+        batch(std::integral_constant<int, 8>{});
+      else if (r > 2)
+        batch(std::integral_constant<int, 4>{});
+      else if (r > 1)
+        batch(std::integral_constant<int, 2>{});
+      else
+        batch(std::integral_constant<int, 1>{});
+    }
     // the inserted entries into their marked positions, after every old
     // entry has moved out of the way
     if (placed) A[P.p] = P.nkey;
