@@ -407,6 +407,7 @@ void open_handle(const gann_config* cfg, gann_handle* h) {
   h->ix.medoid = L.medoid;
   h->ix.R = (int32_t)L.max_m;
   h->ix.dim = (int32_t)L.dim;
+  gann::set_page_divisor(h->ix);
   h->counter_host.alloc(64);
 }
 

@@ -39,7 +39,30 @@ struct IndexDev {
   int64_t medoid;
   int32_t R;
   int32_t dim;
+  // node u's page is u / nodes_per_page = umulhi(u, npp_magic) >> npp_shift
+  // for u < 2^31 (npp_shift < 0: one node per page); set by set_page_divisor
+  uint32_t npp_magic;
+  int32_t npp_shift;
 };
+
+// The page divisor of IndexDev: for 2 <= d = nodes_per_page <= 4096 and
+// l = ceil(log2 d), m = floor(2^(31+l) / d) + 1 < 2^32 gives
+// floor(u / d) = floor(u m / 2^(31+l)) for every u < 2^31 (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994,
+// Theorem 4.2 with N = 31), so one 32x32 high multiply and a shift replace
+// the 64-bit division.
+inline void set_page_divisor(IndexDev& ix) {
+  const uint32_t d = (uint32_t)ix.nodes_per_page;
+  if (d <= 1) {
+    ix.npp_magic = 0;
+    ix.npp_shift = -1;
+    return;
+  }
+  int l = 0;
+  while ((1u << l) < d) ++l;
+  ix.npp_magic = (uint32_t)((1ull << (31 + l)) / d + 1);
+  ix.npp_shift = l - 1;
+}
 
 // Pivot graph resident in HBM.
 struct NavDev {

@@ -21,8 +21,15 @@ namespace gann {
 template <int V>
 using ic = std::integral_constant<int, V>;
 
+// Node u's record: page u / nodes_per_page, slot u % nodes_per_page (node ids
+// are below 2^31; the page by the multiply of set_page_divisor).
+__device__ __forceinline__ uint32_t page_of(const IndexDev& ix, uint32_t u) {
+  return ix.npp_shift < 0 ? u : __umulhi(u, ix.npp_magic) >> ix.npp_shift;
+}
 __device__ __forceinline__ const uint8_t* record_of(const IndexDev& ix, int64_t u) {
-  return ix.pages + (u / ix.nodes_per_page) * 4096 + (u % ix.nodes_per_page) * ix.node_len;
+  const uint32_t n = (uint32_t)u, page = page_of(ix, n);
+  const uint32_t slot = n - page * (uint32_t)ix.nodes_per_page;
+  return ix.pages + ((uint64_t)page << 12) + slot * (uint32_t)ix.node_len;
 }
 
 // Rerank coordinates per lane kept in registers by the kernels with one
@@ -822,7 +829,8 @@ __global__ __launch_bounds__(64) void step_round_kernel(IndexDev ix, PQDev pq,
   // the record comes from the index pages, or from this query's 4096-byte
   // slot that the host filled with u's page (src/hyd_task_runner.cu:216-240)
   if (slots)
-    cur.load_at(ix, slots + (int64_t)qi * kStepSlotBytes + (u % ix.nodes_per_page) * ix.node_len);
+    cur.load_at(ix, slots + (int64_t)qi * kStepSlotBytes +
+                        ((uint32_t)u - page_of(ix, (uint32_t)u) * (uint32_t)ix.nodes_per_page) * (uint32_t)ix.node_len);
   else
     cur.load(ix, u);
   const float* qq = q + (int64_t)qi * dim;
