@@ -461,6 +461,10 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
 
 constexpr int kGpWide = kCbGpWide;
 
+// s_waitcnt operand: vmcnt(0), expcnt and lgkmcnt not waited for (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int kVmcntZero = 0x0F70;
+
 // Largest workgroup of the shared-codebook kernels: 16 waves, or 8 when a
 // lane keeps more than 8 rerank coordinates or all pivot rows of a lookup
 // (kGpWide) in flight (the 128-VGPR cap of 16-wave workgroups would spill
@@ -559,8 +563,9 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
     // one the plain loop loads.  The guess loads come after the loads the
     // expansion waits for, so they never hold those up.
     constexpr bool kSpec = cb_is_wide(kSplitG) && NB == 1;
-    CodeRow<MW> rows;       // cur's code rows (lanes past deg: all codes 0)
-    bool rows_ok = false;   // rows already requested for cur (uniform)
+    struct NoPivots {};
+    std::conditional_t<kSpec, WidePivots<(kSpec ? MW : 1), (kSpec ? W : 4), kWL>, NoPivots> wp;  // cur's pivot rows
+    bool piv_ok = false;    // wp already requested for cur (uniform)
     RecRegs<T, KP, NB> gs;  // the guessed next node's record
     CodeRow<MW> grows;      // and its code rows
     int32_t g_id = -1;      // the guess (-1: none)
@@ -570,14 +575,14 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
       adcs += deg;
       uint64_t key[NB];
       if constexpr (kSpec) {
-        if (!rows_ok) {
+        if (!piv_ok) {
+          CodeRow<MW> rows;  // cur's code rows (lanes past deg: all codes 0)
           if (lane < deg)
             rows.load(pq.codes + (int64_t)cur.v[0] * M, M);
           else
             rows.zero();
+          wp.issue(piv, rowb, rows);
         }
-        WidePivots<MW, W, kWL> wp;
-        wp.issue(piv, rowb, rows);
         // the fences keep this order: pivot reads, guess record, the sum
         // (waiting for the pivot reads only), then the first use of the
         // guess record
@@ -611,22 +616,38 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
       const int32_t next =
           __builtin_amdgcn_readfirstlane(P.cand >= 0 ? (int32_t)entry_id(P.sel) : -1);
       RecRegs<T, KP, NB> nxt;
-      bool nrows_ok = false;
+      piv_ok = false;
+      // the guess's code rows (requested an expansion step ago) are waited
+      // for on every path, before the branch: with a load still pending on
+      // one path, the list update below would wait for it, and in issue
+      // order that wait also covers the pivot reads issued early on the
+      // other path
+      if constexpr (kSpec) __builtin_amdgcn_s_waitcnt(kVmcntZero);
       if (kSpec && next >= 0 && next == g_id) {
         nxt = gs;
-        rows = grows;
-        nrows_ok = true;
+        if constexpr (kSpec) {
+          // next's code rows are here: its pivot reads go out now and
+          // arrive during the list update
+          wp.issue(piv, rowb, grows);
+          piv_ok = true;
+          asm volatile("" ::: "memory");
+        }
+      } else if constexpr (kSpec) {
+        // no early pivot reads (a wrong guess, or the last expansion): next's
+        // record is requested after the list update, so that the update has
+        // no pending load on either path
       } else if (next >= 0) {
         nxt.load(ix, next);
       }
       fu = list_apply(A, BM, P);
+      if constexpr (kSpec)
+        if (next >= 0 && !piv_ok) nxt.load(ix, next);
       sz = P.nsz;
       top.push(du, u);
       if constexpr (kSpec)
         g_id = next >= 0 && fu < sz ? __builtin_amdgcn_readfirstlane((int32_t)entry_id(A[fu])) : -1;
       u = next;
       cur = nxt;
-      rows_ok = nrows_ok;
     }
     top.store(nns, dists, qi);
     if (lane == 0) {
