@@ -811,6 +811,11 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
     const int groups = Ly.max_m <= 64 ? gann::search_cb_split_groups(h->pq.dev.M, chunk_w) : 0;
     bool gp = mode == GANN_MODE_FUSED_GP || (w_lds < kMinLdsWaves && w_gp > w_lds);
     int g = 0;
+    // Failing that, the half table while it keeps kHalfWaves lists: at dim
+    // 128 it beats the wide form below down to 7 lists (10M index: L=1152,
+    // 9 lists, 25.0 against 29.0 ms; L=1408, 7 lists, 32.2 against 35.5 ms;
+    // L=1536 even) and loses at 6 (L=1664, 44.8 against 41.0 ms).
+    constexpr int kHalfWaves = 7;
     if (mode == GANN_MODE_FUSED && w_lds < kSplitWaves && groups > 1) {
       for (int c : {groups - 1, groups / 2})
         if (gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, true, c) >= kSplitWaves) {
@@ -818,12 +823,19 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
           gp = true;
           break;
         }
+      if (g == 0 && gann::search_cb_waves(D, M, cw, L, topk, h->lds_limit, true, groups / 2) >= kHalfWaves) {
+        g = groups / 2;
+        gp = true;
+      }
     }
-    // Once at most 8 lists fit per CU beside no table (L >= ~2000 at dim
-    // 128), the registers of 8-wave workgroups hold every pivot row of a
-    // lookup in flight (the wide form).
+    // Where the table would be read through the caches (no split keeps
+    // enough lists), the wide form: 8-wave workgroups with every pivot row
+    // of a lookup in flight and the first chunks in the LDS the lists leave.
+    // Measured on uint8 dim-128 indexes it beats the cache-read form with
+    // more lists at every L from 1024 to 2048 (10M index, 9-16 lists against
+    // 8: 2-7% faster) and keeps its 8 lists above (7 at L=2576).
     const bool wide_ok = gann::search_cb_wide_ok(M, cw, D);
-    if (mode == GANN_MODE_FUSED && gp && g == 0 && wide_ok && w_gp <= 8) g = gann::kCbGpWide;
+    if (mode == GANN_MODE_FUSED && gp && g == 0 && wide_ok) g = gann::kCbGpWide;
     // tuning override: "split" (all groups but one in LDS), "half",
     // "cache" (none in LDS) or "wide" (none in LDS, wide lookup) forces that
     // form
