@@ -477,10 +477,9 @@ __host__ __device__ constexpr int cb_block_threads(int KP, int kSplitG = 0) {
 // instead of a copy in LDS, which then holds only the per-wave lists: the
 // form for large L, where lists beside a 128 KB table leave few waves.
 // kSplitG > 0 (with kGP): that many groups of 8 chunks also in LDS;
-// kSplitG == kGpWide - G (with kGP): the wide lookup of cb_adc, 8-wave
+// kSplitG == kGpWide - G (with kGP): the wide lookup of cb_adc in 8-wave
 // workgroups, the first G chunks (one neighbour block only) from a partial
-// table in LDS;
-// workgroups.  KP: rerank coordinates per lane held in registers; NB:
+// table in LDS.  KP: rerank coordinates per lane held in registers; NB:
 // neighbour blocks.
 template <typename T, int MW, int W, bool kGP, int kSplitG, int KP, int NB>
 __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kernel(
@@ -632,14 +631,13 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
           piv_ok = true;
           asm volatile("" ::: "memory");
         }
-      } else if constexpr (kSpec) {
-        // no early pivot reads (a wrong guess, or the last expansion): next's
-        // record is requested after the list update, so that the update has
-        // no pending load on either path
-      } else if (next >= 0) {
+      } else if (!kSpec && next >= 0) {
         nxt.load(ix, next);
       }
       fu = list_apply(A, BM, P);
+      // kSpec without early pivot reads (a wrong guess): next's record is
+      // requested after the list update, so that the update has no pending
+      // load on either path
       if constexpr (kSpec)
         if (next >= 0 && !piv_ok) nxt.load(ix, next);
       sz = P.nsz;
