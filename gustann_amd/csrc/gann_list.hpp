@@ -170,8 +170,8 @@ __device__ __forceinline__ ListPlan list_plan(const uint64_t* A, int L, uint64_t
 // positions the inserted entries take are marked in the bitmap BM; output
 // position j then holds inserted entry nb(j) (nb = inserted entries placed
 // before j) if marked, else old entry j - nb(j).  The old entries are
-// gathered into the unmarked positions in batches of 16 chunks, top batch
-// first (near the start of the list the last one may be of 8, 4, 2 or 1):
+// gathered into the unmarked positions in windows of 16 chunks, top window
+// first (near the start of the list the last ones may be of 8, 4, 2 or 1):
 // a batch reads only positions below its highest output and at or above its
 // lowest output minus 64, and writes after all its reads, so no source is
 // overwritten before it is read; chunks below the first insertion that a
@@ -217,15 +217,17 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
     // a batch before its writes.  Full windows of kBatch chunks [b_hi - 16,
     // b_hi) from the top: the chunk of each slot, its mask word in the batch's
     // read and its LDS offset are fixed at compile time.
+    // One full window of kB chunks [b_hi - kB, b_hi) (b_hi >= kB).
     int b_hi = ct + 1;
-    while (b_hi > cb && b_hi >= kBatch) {
-      const int b_lo = b_hi - kBatch;
-      const uint32_t wv = lane < 2 * kBatch ? BM[2 * b_lo + lane] : 0u;
+    auto window = [&](auto kb) {
+      constexpr int kB = decltype(kb)::value;
+      const int b_lo = b_hi - kB;
+      const uint32_t wv = lane < 2 * kB ? BM[2 * b_lo + lane] : 0u;
       const int jtop = kWave * (b_hi - 1) + lane;
-      uint64_t val[kBatch];
+      uint64_t val[kB];
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        constexpr int kTop = 2 * (kBatch - 1);
+      for (int t = 0; t < kB; ++t) {
+        constexpr int kTop = 2 * (kB - 1);
         const uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, kTop - 2 * t + 1) << 32) |
                             (uint32_t)__builtin_amdgcn_readlane((int)wv, kTop - 2 * t);
         below -= __popcll(mo);
@@ -233,49 +235,19 @@ __device__ __forceinline__ int list_apply(uint64_t* A, uint32_t* BM, const ListP
       }
       wave_sync();
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) A[jtop - kWave * t] = val[t];
+      for (int t = 0; t < kB; ++t) A[jtop - kWave * t] = val[t];
       wave_sync();
       b_hi = b_lo;
-    }
-    // What is left lies in the first kBatch - 1 chunks of the list: one
-    // batch of 16, 8, 4, 2 or 1 chunks [max(0, b_hi - kB), b_hi), the
-    // smallest that reaches cb; slots below chunk 0 repeat chunk 0 (the same
-    // reads and writes twice).
-    if (b_hi > cb) {
-      auto batch = [&](auto kb) {
-        constexpr int kB = decltype(kb)::value;
-        const int b_lo = max(0, b_hi - kB);
-        const uint32_t wv = lane < 2 * (b_hi - b_lo) ? BM[2 * b_lo + lane] : 0u;
-        uint64_t val[kB];
-        int dst[kB];
-#pragma unroll
-        for (int t = 0; t < kB; ++t) {
-          const bool rep = b_hi - 1 - t < b_lo;     // uniform
-          const int c = rep ? b_lo : b_hi - 1 - t;  // chunk, top first
-          const int tw = c - b_lo;
-          const uint64_t mo = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw + 1) << 32) |
-                              (uint32_t)__builtin_amdgcn_readlane((int)wv, 2 * tw);
-          if (!rep) below -= __popcll(mo);
-          dst[t] = kWave * c + lane;
-          gather(mo, dst[t], val[t]);
-        }
-        wave_sync();
-#pragma unroll
-        for (int t = 0; t < kB; ++t) A[dst[t]] = val[t];
-        wave_sync();
-      };
-      const int r = b_hi - cb;
-      if (r > 8)
-        batch(std::integral_constant<int, kBatch>{});
-      else if (r > 4)
-        batch(std::integral_constant<int, 8>{});
-      else if (r > 2)
-        batch(std::integral_constant<int, 4>{});
-      else if (r > 1)
-        batch(std::integral_constant<int, 2>{});
-      else
-        batch(std::integral_constant<int, 1>{});
-    }
+    };
+    while (b_hi > cb && b_hi >= kBatch) window(std::integral_constant<int, kBatch>{});
+    // What is left lies in the first kBatch - 1 chunks of the list (so c0 is
+    // chunk 0 and every chunk below cb copies onto itself): windows of 8, 4,
+    // 2 and 1 chunks down from b_hi, each taken while chunks above cb remain
+    // and it fits above chunk 0 -- usually one, at most four.
+    if (b_hi > cb && b_hi >= 8) window(std::integral_constant<int, 8>{});
+    if (b_hi > cb && b_hi >= 4) window(std::integral_constant<int, 4>{});
+    if (b_hi > cb && b_hi >= 2) window(std::integral_constant<int, 2>{});
+    if (b_hi > cb && b_hi >= 1) window(std::integral_constant<int, 1>{});
     // the inserted entries into their marked positions, after every old
     // entry has moved out of the way
     if (placed) A[P.p] = P.nkey;

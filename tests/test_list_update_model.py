@@ -198,3 +198,35 @@ def test_device_rank_is_lower_bound(seed):
                 assert at_r == A[min(r, sz - 1)], (sz, key)
             if sz > 8:
                 assert reads <= 16
+
+
+def test_shift_windows_cover_the_changed_chunks():
+    """list_apply's windows (gann_list.hpp): full 16-chunk windows from the top
+    chunk ct down while chunks at or above cb (the first insertion's chunk)
+    remain and the window fits above chunk 0, then windows of 8, 4, 2 and 1
+    chunks under the same two conditions.  Every chunk from cb to ct is
+    gathered exactly once, top window first; the windows stay inside
+    [c0, ct], c0 = max(0, cb - 15), the chunks whose marks are cleared (those
+    below cb copy onto themselves); at most 4 windows follow the 16-chunk
+    ones."""
+    for ct in range(0, 80):
+        for cb in range(0, ct + 1):
+            c0 = max(0, cb - 15)
+            b_hi, wins = ct + 1, []
+            while b_hi > cb and b_hi >= 16:
+                wins.append((b_hi - 16, b_hi))
+                b_hi -= 16
+            n16 = len(wins)
+            for kb in (8, 4, 2, 1):
+                if b_hi > cb and b_hi >= kb:
+                    wins.append((b_hi - kb, b_hi))
+                    b_hi -= kb
+            assert b_hi <= cb, (ct, cb)
+            assert len(wins) - n16 <= 4
+            covered = []
+            for lo, hi in wins:
+                assert c0 <= lo < hi <= ct + 1, (ct, cb, lo, hi)
+                covered += list(range(hi - 1, lo - 1, -1))
+            assert covered == sorted(covered, reverse=True)      # top down, no overlap
+            assert set(range(cb, ct + 1)) <= set(covered)
+            assert len(covered) == len(set(covered))
