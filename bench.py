@@ -506,8 +506,8 @@ MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8
 def bench_knn(args):
     """Exact k-NN (ground truth) of nq uint8 queries over n uint8 points
     (gann_knn_exact, int8 MFMA).  Timed end to end (base upload, kernels,
-    host merge of the slices); operations counted as 2 * n * nq * dim int8
-    multiply-adds."""
+    the merge of the slices on the device, result download); operations
+    counted as 2 * n * nq * dim int8 multiply-adds."""
     import torch  # noqa: F401  (device runtime first)
     from gustann_amd import index as gi
     n, dim, nq, k = args.n, args.dim, args.nq, args.knn_k

@@ -1303,17 +1303,22 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
     const int nqp = (nq + QB - 1) / QB * QB;
     const int dp = (dim + 31) / 32 * 32;
     const size_t elem = u8 ? 1 : 4;
-    const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t)1 << 31) / (dim * (int64_t)elem)));
+    int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t)1 << 31) / (dim * (int64_t)elem)));
+    if (const char* e = std::getenv("GANN_KNN_CHUNK"))  // smaller chunks: tests of the chunk merge
+      chunk = std::max<int64_t>(1, std::min<int64_t>(chunk, std::atoll(e)));
     const int64_t qblocks = nqp / QB;
     // about 8 wavefronts per CU, each slice at least 1024 points
     int64_t slices = std::max<int64_t>(1, std::min<int64_t>((8LL * cus + qblocks - 1) / qblocks,
                                                            (chunk + 1023) / 1024));
     const int64_t slice_len = ((chunk + slices - 1) / slices + 31) / 32 * 32;
     slices = (chunk + slice_len - 1) / slice_len;
+    // part_d/part_i hold [slices + 1][nq][k]: slot 0 keeps the best of the
+    // chunks merged so far, a chunk's slices go to slots 1.. (0.. for the
+    // first chunk) and are merged into slot 0 on the device
     DevBuf raw, xs, xn, qs, qn, qf, pd, pi;
     raw.ensure((size_t)chunk * dim * elem);
-    pd.ensure((size_t)slices * nq * k * 4);
-    pi.ensure((size_t)slices * nq * k * 4);
+    pd.ensure((size_t)(slices + 1) * nq * k * 4);
+    pi.ensure((size_t)(slices + 1) * nq * k * 4);
     if (u8) {
       std::vector<int8_t> hq((size_t)nqp * dp, 0);
       std::vector<int32_t> hn((size_t)nqp, 0);
@@ -1337,46 +1342,27 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
       GANN_HIP(hipMemcpy(qf.p, queries, (size_t)nq * dim * 4, hipMemcpyHostToDevice));
     }
     check_lds(gann::knn_smem_bytes(u8 ? 0 : 1, dim, k), device_id, "exact k-NN");
-    std::vector<float> bd((size_t)nq * k, INFINITY), hd((size_t)slices * nq * k);
-    std::vector<int32_t> bi((size_t)nq * k, -1), hi((size_t)slices * nq * k);
-    std::vector<std::pair<float, int32_t>> cand;
     for (int64_t off = 0; off < n; off += chunk) {
       const int64_t cn = std::min(chunk, n - off);
       const int64_t cs = (cn + slice_len - 1) / slice_len;
+      const int64_t s0 = off == 0 ? 0 : 1;
+      float* sd = pd.as<float>() + (size_t)s0 * nq * k;
+      int32_t* si = pi.as<int32_t>() + (size_t)s0 * nq * k;
       GANN_HIP(hipMemcpy(raw.p, (const uint8_t*)base + (size_t)off * dim * elem, (size_t)cn * dim * elem,
                          hipMemcpyHostToDevice));
       if (u8) {
         GANN_HIP(gann::launch_knn_prep_u8(raw.as<uint8_t>(), cn, dim, dp, xs.as<int8_t>(),
                                           xn.as<int32_t>(), 0));
         GANN_HIP(gann::launch_knn_u8(xs.as<int8_t>(), xn.as<int32_t>(), cn, dp, qs.as<int8_t>(),
-                                     qn.as<int32_t>(), nq, k, cs, slice_len, off, pd.as<float>(),
-                                     pi.as<int32_t>(), 0));
+                                     qn.as<int32_t>(), nq, k, cs, slice_len, off, sd, si, 0));
       } else {
         GANN_HIP(gann::launch_knn_f32(raw.as<float>(), cn, dim, qf.as<float>(), nq, k, cs, slice_len,
-                                      off, pd.as<float>(), pi.as<int32_t>(), 0));
+                                      off, sd, si, 0));
       }
-      GANN_HIP(hipMemcpy(hd.data(), pd.p, (size_t)cs * nq * k * 4, hipMemcpyDeviceToHost));
-      GANN_HIP(hipMemcpy(hi.data(), pi.p, (size_t)cs * nq * k * 4, hipMemcpyDeviceToHost));
-      for (int32_t q = 0; q < nq; ++q) {
-        cand.clear();
-        for (int32_t j = 0; j < k; ++j)
-          if (bi[(size_t)q * k + j] >= 0) cand.emplace_back(bd[(size_t)q * k + j], bi[(size_t)q * k + j]);
-        for (int64_t sl = 0; sl < cs; ++sl)
-          for (int32_t j = 0; j < k; ++j) {
-            const size_t o = ((size_t)sl * nq + q) * k + j;
-            if (hi[o] >= 0) cand.emplace_back(hd[o], hi[o]);
-          }
-        const size_t keep = std::min<size_t>(cand.size(), (size_t)k);
-        std::partial_sort(cand.begin(), cand.begin() + keep, cand.end());
-        for (int32_t j = 0; j < k; ++j) {
-          const bool ok = (size_t)j < keep;
-          bd[(size_t)q * k + j] = ok ? cand[(size_t)j].first : INFINITY;
-          bi[(size_t)q * k + j] = ok ? cand[(size_t)j].second : -1;
-        }
-      }
+      GANN_HIP(gann::launch_knn_merge(pd.as<float>(), pi.as<int32_t>(), nq, k, s0 + cs, 0));
     }
-    std::memcpy(ids, bi.data(), bi.size() * 4);
-    std::memcpy(dists, bd.data(), bd.size() * 4);
+    GANN_HIP(hipMemcpy(ids, pi.p, (size_t)nq * k * 4, hipMemcpyDeviceToHost));
+    GANN_HIP(hipMemcpy(dists, pd.p, (size_t)nq * k * 4, hipMemcpyDeviceToHost));
   });
 }
 

@@ -109,6 +109,10 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// s_waitcnt operand: vmcnt(0), expcnt and lgkmcnt not waited for (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int kVmcntZero = 0x0F70;
+
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
 // Inclusive prefix sum over the 64 lanes: DPP row_shr 1/2/4/8 inside each

@@ -14,7 +14,7 @@
 // LDS buffer; a buffer that could overflow with the next tile is cut back to
 // its k best by rank.  Points are scanned in increasing id order, so a tie
 // with the k-th best loses to it.  Each wavefront writes its sorted k best
-// per query; the host merges the slices.
+// per query; a tree of pairwise merges on the device folds the slices.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -31,6 +31,8 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kQB = 32;  // queries per wavefront (MFMA rows)
 constexpr int kTP = 32;  // points per tile (MFMA columns)
+constexpr int kPF = 4;   // uint8 tiles in flight per wavefront
+constexpr int kMaxK = 128;
 
 // Row of accumulator register i of this lane in a 32x32 MFMA result (the
 // column is lane % 32).
@@ -176,8 +178,8 @@ __global__ void knn_prep_u8_wide_kernel(const uint4* __restrict__ x, int64_t chu
 }
 
 // One 32-point tile of B operands (lane: point t0 + lane % 32, bytes
-// 16 * (lane / 32) + 32 s) and the point's |x'|^2; points past `end` read
-// row `start` and are marked invalid.
+// 16 * (lane / 32) + 32 s) and the point's |x'|^2; points at or past `end`
+// (any distance past it) read row `start` and are marked invalid.
 template <int STEPS>
 struct KnnTile {
   v4i b[STEPS];
@@ -227,38 +229,60 @@ __global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ x
     qn_r[i] = qn[q0 + m];
     thr_r[i] = q0 + m < nq ? INT32_MAX : INT32_MIN;
   }
-  KnnTile<STEPS> cur, nxt;
-  if (start < end) cur.load(xs, xn, start, start, end, lane);
-  for (int64_t t0 = start; t0 < end; t0 += kTP) {
-    if (t0 + kTP < end) nxt.load(xs, xn, t0 + kTP, start, end, lane);  // next tile in flight
-    v16i acc = {};
+  // the query rows and norms are waited for here, before the loop: loads
+  // left pending into it would make their first uses there wait on the tile
+  // loads too, on every tile
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s)
-      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], cur.b[s], acc, 0, 0, 0);
-    int32_t dist[16];
-    uint64_t any = 0;
+  for (int s = 0; s < STEPS; ++s) asm volatile("" ::"v"(a[s]));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      dist[i] = qn_r[i] + cur.xn - 2 * acc[i];
-      any |= ballot64(cur.valid && dist[i] < thr_r[i]);
-    }
-    if (any) {
-      const int32_t id = (int32_t)(t0 + (lane & 31) + id_base);
+  for (int i = 0; i < 16; ++i) asm volatile("" ::"v"(qn_r[i]));
+  // kPF tiles in flight: tile t0 is used kPF tiles after its loads were
+  // issued.  The loads are unconditional (tiles past the slice read row
+  // `start`, marked invalid), so every path through the loop has the same
+  // loads outstanding and the wait before a tile's products covers only
+  // that tile.
+  // (the first kPF are requested in tile order, as the loop requests them,
+  // so the wait at the loop head is the same from either side)
+  KnnTile<STEPS> tl[kPF];
+#pragma unroll
+  for (int u = 0; u < kPF; ++u) {
+    tl[u].load(xs, xn, start + u * kTP, start, end, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int64_t g = start; g < end; g += kPF * kTP) {
+#pragma unroll
+    for (int u = 0; u < kPF; ++u) {
+      const int64_t t0 = g + u * kTP;
+      v16i acc = {};
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s)
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], tl[u].b[s], acc, 0, 0, 0);
+      const bool valid = tl[u].valid;
+      int32_t dist[16];
+      uint64_t any = 0;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        if (cur.valid && dist[i] < thr_r[i]) B.append(acc_row(i, lane), (float)dist[i], id);
+        dist[i] = qn_r[i] + tl[u].xn - 2 * acc[i];
+        any |= ballot64(valid && dist[i] < thr_r[i]);
       }
-      wave_sync();
-      if (B.maybe_compact()) {
+      tl[u].load(xs, xn, t0 + kPF * kTP, start, end, lane);
+      if (any) {
+        const int32_t id = (int32_t)(t0 + (lane & 31) + id_base);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int m = acc_row(i, lane);
-          const float t = B.thr[m];
-          if (q0 + m < nq) thr_r[i] = t == INFINITY ? INT32_MAX : (int32_t)t;
+          if (valid && dist[i] < thr_r[i]) B.append(acc_row(i, lane), (float)dist[i], id);
+        }
+        wave_sync();
+        if (B.maybe_compact()) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int m = acc_row(i, lane);
+            const float t = B.thr[m];
+            if (q0 + m < nq) thr_r[i] = t == INFINITY ? INT32_MAX : (int32_t)t;
+          }
         }
       }
     }
-    cur = nxt;
   }
   B.finish(q0, nq, slice, part_d, part_i);
 }
@@ -313,9 +337,69 @@ __global__ __launch_bounds__(64) void knn_f32_kernel(const float* __restrict__ x
   B.finish(q0, nq, slice, part_d, part_i);
 }
 
+// One level of the slice merge: for query blockIdx.x, the sorted k-lists of
+// slots a and b = a + stride (a = 2 * stride * blockIdx.y) become the first k
+// of their union in (dist, id) order, written to slot a.  Entry j of list A
+// goes to j + #{B < A[j]}, entry j of B to j + #{A <= B[j]}: a stable merge,
+// so the padding entries (+inf, -1), all equal, still take distinct places
+// and order after every real entry.  Both lists are read into LDS before any
+// write, and each block owns its two slots.
+__global__ __launch_bounds__(64) void knn_merge_kernel(float* __restrict__ part_d,
+                                                       int32_t* __restrict__ part_i, int nq, int k,
+                                                       int64_t slots, int64_t stride) {
+  __shared__ uint64_t ka[kMaxK], kb[kMaxK];
+  const int q = blockIdx.x;
+  const int64_t a = (int64_t)blockIdx.y * 2 * stride, b = a + stride;
+  if (b >= slots) return;
+  const int lane = threadIdx.x;
+  const size_t oa = ((size_t)a * nq + q) * k, ob = ((size_t)b * nq + q) * k;
+  for (int j = lane; j < k; j += kWave) {
+    ka[j] = cand_key(part_d[oa + j], part_i[oa + j]);
+    kb[j] = cand_key(part_d[ob + j], part_i[ob + j]);
+  }
+  __syncthreads();
+  for (int j = lane; j < k; j += kWave) {
+    const uint64_t x = ka[j], y = kb[j];
+    int lo = 0, hi = k;
+    while (lo < hi) {
+      const int m = (lo + hi) >> 1;
+      if (kb[m] < x) lo = m + 1; else hi = m;
+    }
+    const int ra = j + lo;
+    lo = 0, hi = k;
+    while (lo < hi) {
+      const int m = (lo + hi) >> 1;
+      if (ka[m] <= y) lo = m + 1; else hi = m;
+    }
+    const int rb = j + lo;
+    if (ra < k) {
+      part_d[oa + ra] = __uint_as_float((uint32_t)(x >> 32));
+      part_i[oa + ra] = (int32_t)(uint32_t)x;
+    }
+    if (rb < k) {
+      part_d[oa + rb] = __uint_as_float((uint32_t)(y >> 32));
+      part_i[oa + rb] = (int32_t)(uint32_t)y;
+    }
+  }
+}
+
 size_t knn_buf_bytes(int k) { return (size_t)kQB * (k + 64) * 8 + (size_t)kQB * 8; }
 
 }  // namespace
+
+hipError_t launch_knn_merge(float* part_d, int32_t* part_i, int nq, int k, int64_t slots,
+                            hipStream_t stream) {
+  if (k < 1 || k > kMaxK || nq < 0) return hipErrorInvalidValue;
+  if (nq == 0) return hipSuccess;
+  for (int64_t stride = 1; stride < slots; stride *= 2) {
+    const dim3 grid((unsigned)nq, (unsigned)((slots + 2 * stride - 1) / (2 * stride)));
+    hipLaunchKernelGGL(knn_merge_kernel, grid, dim3(kWave), 0, stream, part_d, part_i, nq, k, slots,
+                       stride);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 
 int knn_queries_per_block() { return kQB; }
 

@@ -21,6 +21,11 @@ hipError_t launch_knn_prep_u8(const uint8_t* x, int64_t n, int dim, int dp, int8
 hipError_t launch_knn_u8(const int8_t* xs, const int32_t* xn, int64_t n, int dp, const int8_t* qs,
                          const int32_t* qn, int nq, int k, int64_t slices, int64_t slice_len,
                          int64_t id_base, float* part_d, int32_t* part_i, hipStream_t stream);
+// Folds slots [0, slots) of part_d/part_i [slots][nq][k] into slot 0, per
+// query the k best of all of them in (dist, id) order (a tree of pairwise
+// merges, log2(slots) launches).  k <= 128.
+hipError_t launch_knn_merge(float* part_d, int32_t* part_i, int nq, int k, int64_t slots,
+                            hipStream_t stream);
 hipError_t launch_knn_f32(const float* x, int64_t n, int dim, const float* q, int nq, int k,
                           int64_t slices, int64_t slice_len, int64_t id_base, float* part_d,
                           int32_t* part_i, hipStream_t stream);

@@ -461,10 +461,6 @@ __device__ __forceinline__ float cb_adc(const uint8_t* piv, const float* qs, uin
 
 constexpr int kGpWide = kCbGpWide;
 
-// s_waitcnt operand: vmcnt(0), expcnt and lgkmcnt not waited for (gfx9
-// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
-constexpr int kVmcntZero = 0x0F70;
-
 // Largest workgroup of the shared-codebook kernels: 16 waves, or 8 when a
 // lane keeps more than 8 rerank coordinates or all pivot rows of a lookup
 // (kGpWide) in flight (the 128-VGPR cap of 16-wave workgroups would spill

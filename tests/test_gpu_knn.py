@@ -67,3 +67,29 @@ def test_argument_errors():
         gi.brute_force_knn_gpu(X, Q, 10)      # uint8 queries must be integral
     with pytest.raises(GannError):
         gi.brute_force_knn_gpu(X, np.zeros((2, 16), np.float32), 129)
+
+
+@pytest.mark.parametrize("chunk", ["700", "12345"])
+def test_chunks_merged_on_the_device(monkeypatch, chunk):
+    # GANN_KNN_CHUNK cuts the base into chunks of that many points (43 and
+    # 3 chunks here, the last one ragged): each chunk's slices are merged
+    # into the running best on the device
+    monkeypatch.setenv("GANN_KNN_CHUNK", chunk)
+    X = _u8(30000, 64, 11)
+    Q = _u8(50, 64, 12).astype(np.float32)
+    for k in (10, 100):
+        g = gi.brute_force_knn_gpu(X, Q, k)
+        c = gi.brute_force_knn(X, Q, k, threads=8)
+        assert np.array_equal(g[0], c[0]) and np.array_equal(g[1], c[1]), k
+    T = _u8(20000, 6, 13, hi=2)                 # ties everywhere
+    Qt = _u8(33, 6, 14, hi=2).astype(np.float32)
+    g = gi.brute_force_knn_gpu(T, Qt, 40)
+    c = gi.brute_force_knn(T, Qt, 40, threads=8)
+    assert np.array_equal(g[0], c[0]) and np.array_equal(g[1], c[1])
+    r = np.random.default_rng(15)
+    F = r.standard_normal((9000, 40)).astype(np.float32)
+    Qf = r.standard_normal((20, 40)).astype(np.float32)
+    g_ids, g_d = gi.brute_force_knn_gpu(F, Qf, 10)
+    c_ids, c_d = gi.brute_force_knn(F, Qf, 10, threads=8)
+    assert (g_ids == c_ids).mean() >= 0.999
+    assert np.allclose(g_d, c_d, rtol=1e-5, atol=0)
