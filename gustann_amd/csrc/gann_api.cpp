@@ -1279,6 +1279,26 @@ int gann_pq_adc_scan_device(gann_pq* pq, const float* q_dev, int32_t nq, const i
 }
 
 
+namespace {
+
+// Slices of a base chunk for the exact k-NN: each (query block, slice) is one
+// wavefront.  The count minimizes ceil(qblocks s / resident) / s, the rounds
+// of resident wavefronts times the points per slice (a last round far from
+// full idles the GPU), over at most 3 rounds (every slice adds candidate
+// insertions), with at least 1024 points per slice; the smallest count on a
+// tie.
+int64_t knn_slices(int64_t qblocks, int64_t resident, int64_t chunk) {
+  const int64_t smax = std::max<int64_t>(1, std::min<int64_t>((chunk + 1023) / 1024, 3 * resident / qblocks));
+  int64_t best = 1, best_r = (qblocks + resident - 1) / resident;
+  for (int64_t s = 2; s <= smax; ++s) {
+    const int64_t r = (qblocks * s + resident - 1) / resident;
+    if (r * best < best_r * s) best = s, best_r = r;
+  }
+  return best;
+}
+
+}  // namespace
+
 int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, const float* queries,
                    int32_t nq, int32_t k, int32_t device_id, int32_t* ids, float* dists) {
   return guarded([&] {
@@ -1299,17 +1319,19 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
     GANN_HIP(hipSetDevice(device_id));
     int cus = 0;
     GANN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_id));
-    const int QB = gann::knn_queries_per_block();
+    const gann::KnnU8Form form = u8 ? gann::knn_u8_form(dim, k) : gann::KnnU8Form{0, 0, 0};
+    if (u8 && form.blocks_per_cu < 1) raise(GANN_ERR_UNSUPPORTED, "exact k-NN kernel does not fit a CU");
+    const int QB = u8 ? form.qb : gann::kKnnF32Queries;
     const int nqp = (nq + QB - 1) / QB * QB;
-    const int dp = (dim + 31) / 32 * 32;
+    const int dp = form.dp;
     const size_t elem = u8 ? 1 : 4;
     int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t)1 << 31) / (dim * (int64_t)elem)));
     if (const char* e = std::getenv("GANN_KNN_CHUNK"))  // smaller chunks: tests of the chunk merge
       chunk = std::max<int64_t>(1, std::min<int64_t>(chunk, std::atoll(e)));
     const int64_t qblocks = nqp / QB;
-    // about 8 wavefronts per CU, each slice at least 1024 points
-    int64_t slices = std::max<int64_t>(1, std::min<int64_t>((8LL * cus + qblocks - 1) / qblocks,
-                                                           (chunk + 1023) / 1024));
+    const int64_t resident =
+        (int64_t)cus * std::max(1, u8 ? form.blocks_per_cu : gann::knn_f32_blocks_per_cu(dim, k));
+    int64_t slices = knn_slices(qblocks, resident, chunk);
     const int64_t slice_len = ((chunk + slices - 1) / slices + 31) / 32 * 32;
     slices = (chunk + slice_len - 1) / slice_len;
     // part_d/part_i hold [slices + 1][nq][k]: slot 0 keeps the best of the
@@ -1341,7 +1363,7 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
       qf.ensure((size_t)nq * dim * 4);
       GANN_HIP(hipMemcpy(qf.p, queries, (size_t)nq * dim * 4, hipMemcpyHostToDevice));
     }
-    check_lds(gann::knn_smem_bytes(u8 ? 0 : 1, dim, k), device_id, "exact k-NN");
+    check_lds(gann::knn_smem_bytes(u8 ? 0 : 1, QB, u8 ? dp : dim, k), device_id, "exact k-NN");
     for (int64_t off = 0; off < n; off += chunk) {
       const int64_t cn = std::min(chunk, n - off);
       const int64_t cs = (cn + slice_len - 1) / slice_len;
@@ -1353,7 +1375,7 @@ int gann_knn_exact(const void* base, int64_t n, int32_t dim, int32_t dtype, cons
       if (u8) {
         GANN_HIP(gann::launch_knn_prep_u8(raw.as<uint8_t>(), cn, dim, dp, xs.as<int8_t>(),
                                           xn.as<int32_t>(), 0));
-        GANN_HIP(gann::launch_knn_u8(xs.as<int8_t>(), xn.as<int32_t>(), cn, dp, qs.as<int8_t>(),
+        GANN_HIP(gann::launch_knn_u8(form, xs.as<int8_t>(), xn.as<int32_t>(), cn, qs.as<int8_t>(),
                                      qn.as<int32_t>(), nq, k, cs, slice_len, off, sd, si, 0));
       } else {
         GANN_HIP(gann::launch_knn_f32(raw.as<float>(), cn, dim, qf.as<float>(), nq, k, cs, slice_len,

@@ -3,13 +3,15 @@
 // takes its ground truth from external tools; this is the GPU counterpart of
 // the repository's CPU brute force (index_builder.cpp gib_brute_force).
 //
-// One wavefront owns 32 queries and a slice of the base set and scans it in
-// tiles of 32 points.
-//  * uint8: the 32x32 tile of dot products comes from v_mfma_i32_32x32x32_i8
-//    on x - 128 and q - 128 (int8), so ||q - x||^2 = |q'|^2 + |x'|^2 - 2 q'.x'
-//    is exact in int32 (at most 256 * 255^2 < 2^24, exact again as float).
-//  * float: every lane forms 16 distances directly, sum over the dims in
-//    ascending order of fma(t, t, s), t = q - x.
+// One wavefront owns a block of queries and a slice of the base set and
+// scans it in tiles of 32 points.
+//  * uint8: 16 queries; the two 16x16 blocks of dot products of a tile come
+//    from v_mfma_i32_16x16x64_i8 on x - 128 and q - 128 (int8), so
+//    ||q - x||^2 = |q'|^2 + |x'|^2 - 2 q'.x' is exact in int32 (at most
+//    256 * 255^2 < 2^24, exact again as float).  16 queries rather than 32
+//    halve the candidate buffers, so more wavefronts fit a CU's LDS.
+//  * float: 32 queries; every lane forms 16 distances directly, sum over the
+//    dims in ascending order of fma(t, t, s), t = q - x.
 // A distance below the query's current k-th best is appended to the query's
 // LDS buffer; a buffer that could overflow with the next tile is cut back to
 // its k best by rank.  Points are scanned in increasing id order, so a tie
@@ -27,18 +29,18 @@ namespace gann {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kQB = 32;  // queries per wavefront (MFMA rows)
-constexpr int kTP = 32;  // points per tile (MFMA columns)
-constexpr int kPF = 4;   // uint8 tiles in flight per wavefront
+constexpr int kQB = 32;   // float: queries per wavefront
+constexpr int kTP = 32;   // points per tile
+constexpr int kPF = 4;    // uint8 tiles in flight per wavefront
 constexpr int kMaxK = 128;
 
-// Row of accumulator register i of this lane in a 32x32 MFMA result (the
-// column is lane % 32).
+// The query of distance i of this lane in a 32x32 block (the point is
+// lane % 32): the layout of a 32x32 MFMA result, used by the float kernel too.
 __device__ __forceinline__ int acc_row(int i, int lane) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
 }
+
 
 // Candidate key: bits(dist) << 32 | id.  Distances are non-negative and ids
 // non-negative, so one unsigned compare orders (dist, id) lexicographically.
@@ -46,9 +48,10 @@ __device__ __forceinline__ uint64_t cand_key(float d, int32_t id) {
   return ((uint64_t)__float_as_uint(d) << 32) | (uint32_t)id;
 }
 
-// Per-wavefront candidate buffers: query m keeps keys [0, cnt[m]) of
-// bk[m * cap ...]; thr[m] is the k-th smallest kept distance once k are kept
-// (+inf before).  cap = k + 64 >= k + one tile.
+// Per-wavefront candidate buffers of QB queries: query m keeps keys
+// [0, cnt[m]) of bk[m * cap ...]; thr[m] is the k-th smallest kept distance
+// once k are kept (+inf before).  cap = k + 64 >= k + one tile.
+template <int QB>
 struct KnnBuf {
   uint64_t* bk;
   int32_t* cnt;
@@ -57,7 +60,7 @@ struct KnnBuf {
 
   __device__ void init() {
     const int lane = lane_id();
-    if (lane < kQB) {
+    if (lane < QB) {
       cnt[lane] = 0;
       thr[lane] = INFINITY;
     }
@@ -107,7 +110,7 @@ struct KnnBuf {
   // whether any was cut.
   __device__ bool maybe_compact() {
     const int lane = lane_id();
-    uint64_t need = ballot64(lane < kQB && cnt[lane] > cap - kTP);
+    uint64_t need = ballot64(lane < QB && cnt[lane] > cap - kTP);
     const bool any = need != 0;
     while (need) {
       const int m = (int)__builtin_ctzll(need);
@@ -119,7 +122,7 @@ struct KnnBuf {
 
   __device__ void finish(int q0, int nq, int64_t slice, float* part_d, int32_t* part_i) {
     const int lane = lane_id();
-    for (int m = 0; m < kQB && q0 + m < nq; ++m) {
+    for (int m = 0; m < QB && q0 + m < nq; ++m) {
       compact(m);
       const int n = cnt[m];
       const int64_t o = (slice * nq + q0 + m) * (int64_t)k;
@@ -132,13 +135,14 @@ struct KnnBuf {
   }
 };
 
-__device__ __forceinline__ KnnBuf knn_buf(uint8_t* smem, int k) {
-  KnnBuf B;
+template <int QB>
+__device__ __forceinline__ KnnBuf<QB> knn_buf(uint8_t* smem, int k) {
+  KnnBuf<QB> B;
   B.k = k;
   B.cap = k + 64;
   B.bk = reinterpret_cast<uint64_t*>(smem);
-  B.cnt = reinterpret_cast<int32_t*>(B.bk + (size_t)kQB * B.cap);
-  B.thr = reinterpret_cast<float*>(B.cnt + kQB);
+  B.cnt = reinterpret_cast<int32_t*>(B.bk + (size_t)QB * B.cap);
+  B.thr = reinterpret_cast<float*>(B.cnt + QB);
   return B;
 }
 
@@ -177,28 +181,84 @@ __global__ void knn_prep_u8_wide_kernel(const uint4* __restrict__ x, int64_t chu
   atomicAdd(&xn[c / cpr], s);
 }
 
-// One 32-point tile of B operands (lane: point t0 + lane % 32, bytes
-// 16 * (lane / 32) + 32 s) and the point's |x'|^2; points at or past `end`
-// (any distance past it) read row `start` and are marked invalid.
+// The two uint8 forms.  A form fixes the queries per wavefront QB, the K
+// bytes of one product step (kK = 1024 / QB: 64 lanes x 16 bytes cover QB
+// rows), and where each of a lane's kND distances of a 32-point tile sits:
+// its query (one of the lane's kNR query slots) and its column block h
+// (points t0 + QB h + lane % QB).  Lane l holds bytes 16 (l / QB) + kK s of
+// query row l % QB and of the points of its column, the same K bytes on
+// both sides, so every product is a whole dot product.
+template <int QB, int STEPS>
+struct U8Form;
+
+// 32 queries: one 32x32 block per tile from v_mfma_i32_32x32x32_i8;
+// distance i is query 8 (i / 4) + 4 (lane / 32) + i % 4.  Reads each point
+// once per 32 queries.
 template <int STEPS>
-struct KnnTile {
-  v4i b[STEPS];
-  int32_t xn;
-  bool valid;
-  __device__ __forceinline__ void load(const int8_t* xs, const int32_t* xnorm, int64_t t0,
-                                       int64_t start, int64_t end, int lane) {
-    constexpr int dp = 32 * STEPS;
-    const int64_t p = t0 + (lane & 31);
-    const int64_t r = p < end ? p : start;
-    const int8_t* xrow = xs + r * dp + 16 * (lane >> 5);
+struct U8Form<32, STEPS> {
+  static constexpr int kK = 32, kH = 1, kND = 16, kNR = 16;
+  static __device__ __forceinline__ int slot(int i) { return i; }
+  static __device__ __forceinline__ int block(int) { return 0; }
+  static __device__ __forceinline__ int row(int r, int lane) { return acc_row(r, lane); }
+  static __device__ __forceinline__ void products(const v4i* a, const v4i (*b)[STEPS], int32_t* dot) {
+    typedef int v16i __attribute__((ext_vector_type(16)));
+    v16i acc = {};
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) b[s] = *reinterpret_cast<const v4i*>(xrow + 32 * s);
-    xn = xnorm[r];
-    valid = p < end;
+    for (int s = 0; s < STEPS; ++s) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], b[0][s], acc, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kND; ++i) dot[i] = acc[i];
   }
 };
 
+// 16 queries: two 16x16 blocks per tile from v_mfma_i32_16x16x64_i8;
+// distance i is query 4 (lane / 16) + i % 4 of block i / 4.  Half the
+// candidate buffers of the 32-query form, so more wavefronts fit a CU's LDS
+// when k is large, for twice the point reads.
 template <int STEPS>
+struct U8Form<16, STEPS> {
+  static constexpr int kK = 64, kH = 2, kND = 8, kNR = 4;
+  static __device__ __forceinline__ int slot(int i) { return i & 3; }
+  static __device__ __forceinline__ int block(int i) { return i >> 2; }
+  static __device__ __forceinline__ int row(int r, int lane) { return 4 * (lane >> 4) + r; }
+  static __device__ __forceinline__ void products(const v4i* a, const v4i (*b)[STEPS], int32_t* dot) {
+    v4i acc[2] = {};
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s)
+        acc[h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[s], b[h][s], acc[h], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kND; ++i) dot[i] = acc[i >> 2][i & 3];
+  }
+};
+
+// One 32-point tile of B operands (column block h: points t0 + QB h + lane %
+// QB, bytes 16 (lane / QB) + kK s of each) and the points' |x'|^2; points at
+// or past `end` (any distance past it) read row `start` and are marked
+// invalid.
+template <int QB, int STEPS>
+struct KnnTile {
+  using F = U8Form<QB, STEPS>;
+  v4i b[F::kH][STEPS];
+  int32_t xn[F::kH];
+  bool valid[F::kH];
+  __device__ __forceinline__ void load(const int8_t* xs, const int32_t* xnorm, int64_t t0,
+                                       int64_t start, int64_t end, int lane) {
+    constexpr int dp = F::kK * STEPS;
+#pragma unroll
+    for (int h = 0; h < F::kH; ++h) {
+      const int64_t p = t0 + QB * h + lane % QB;
+      const int64_t r = p < end ? p : start;
+      const int8_t* xrow = xs + r * dp + 16 * (lane / QB);
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) b[h][s] = *reinterpret_cast<const v4i*>(xrow + F::kK * s);
+      xn[h] = xnorm[r];
+      valid[h] = p < end;
+    }
+  }
+};
+
+template <int QB, int STEPS>
 __global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ xs,
                                                     const int32_t* __restrict__ xn, int64_t n,
                                                     const int8_t* __restrict__ qs,
@@ -206,28 +266,29 @@ __global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ x
                                                     int64_t slice_len, int64_t id_base,
                                                     float* __restrict__ part_d,
                                                     int32_t* __restrict__ part_i) {
+  using F = U8Form<QB, STEPS>;
   extern __shared__ __align__(16) uint8_t smem_raw[];
-  constexpr int dp = 32 * STEPS;
+  constexpr int dp = F::kK * STEPS;
   const int lane = lane_id();
-  const int q0 = blockIdx.x * kQB;
+  const int q0 = blockIdx.x * QB;
   const int64_t slice = blockIdx.y;
   const int64_t start = slice * slice_len, end = min(n, start + slice_len);
-  KnnBuf B = knn_buf(smem_raw, k);
+  KnnBuf<QB> B = knn_buf<QB>(smem_raw, k);
   B.init();
-  // A: query q0 + lane % 32, bytes 16 * (lane / 32) + 32 s (query rows are
-  // padded to a multiple of 32 on the host)
+  // A: query q0 + lane % QB, bytes 16 * (lane / QB) + kK s (query rows are
+  // padded to a multiple of QB on the host)
   v4i a[STEPS];
-  const int8_t* qrow = qs + (size_t)(q0 + (lane & 31)) * dp + 16 * (lane >> 5);
+  const int8_t* qrow = qs + (size_t)(q0 + lane % QB) * dp + 16 * (lane / QB);
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) a[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
+  for (int s = 0; s < STEPS; ++s) a[s] = *reinterpret_cast<const v4i*>(qrow + F::kK * s);
   // distances are exact integers: thresholds in int32 (rows past nq take
   // nothing)
-  int32_t qn_r[16], thr_r[16];
+  int32_t qn_r[F::kNR], thr_r[F::kNR];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int m = acc_row(i, lane);
-    qn_r[i] = qn[q0 + m];
-    thr_r[i] = q0 + m < nq ? INT32_MAX : INT32_MIN;
+  for (int r = 0; r < F::kNR; ++r) {
+    const int m = F::row(r, lane);
+    qn_r[r] = qn[q0 + m];
+    thr_r[r] = q0 + m < nq ? INT32_MAX : INT32_MIN;
   }
   // the query rows and norms are waited for here, before the loop: loads
   // left pending into it would make their first uses there wait on the tile
@@ -235,15 +296,15 @@ __global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ x
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) asm volatile("" ::"v"(a[s]));
 #pragma unroll
-  for (int i = 0; i < 16; ++i) asm volatile("" ::"v"(qn_r[i]));
+  for (int r = 0; r < F::kNR; ++r) asm volatile("" ::"v"(qn_r[r]));
   // kPF tiles in flight: tile t0 is used kPF tiles after its loads were
   // issued.  The loads are unconditional (tiles past the slice read row
   // `start`, marked invalid), so every path through the loop has the same
   // loads outstanding and the wait before a tile's products covers only
-  // that tile.
-  // (the first kPF are requested in tile order, as the loop requests them,
-  // so the wait at the loop head is the same from either side)
-  KnnTile<STEPS> tl[kPF];
+  // that tile (the first kPF are requested in tile order, as the loop
+  // requests them, so the wait at the loop head is the same from either
+  // side).
+  KnnTile<QB, STEPS> tl[kPF];
 #pragma unroll
   for (int u = 0; u < kPF; ++u) {
     tl[u].load(xs, xn, start + u * kTP, start, end, lane);
@@ -253,32 +314,32 @@ __global__ __launch_bounds__(64) void knn_u8_kernel(const int8_t* __restrict__ x
 #pragma unroll
     for (int u = 0; u < kPF; ++u) {
       const int64_t t0 = g + u * kTP;
-      v16i acc = {};
+      int32_t dist[F::kND];
+      F::products(a, tl[u].b, dist);
+      bool valid[F::kH];
 #pragma unroll
-      for (int s = 0; s < STEPS; ++s)
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], tl[u].b[s], acc, 0, 0, 0);
-      const bool valid = tl[u].valid;
-      int32_t dist[16];
+      for (int h = 0; h < F::kH; ++h) valid[h] = tl[u].valid[h];
       uint64_t any = 0;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        dist[i] = qn_r[i] + tl[u].xn - 2 * acc[i];
-        any |= ballot64(valid && dist[i] < thr_r[i]);
+      for (int i = 0; i < F::kND; ++i) {
+        dist[i] = qn_r[F::slot(i)] + tl[u].xn[F::block(i)] - 2 * dist[i];
+        any |= ballot64(valid[F::block(i)] && dist[i] < thr_r[F::slot(i)]);
       }
       tl[u].load(xs, xn, t0 + kPF * kTP, start, end, lane);
       if (any) {
-        const int32_t id = (int32_t)(t0 + (lane & 31) + id_base);
+        const int32_t id = (int32_t)(t0 + lane % QB + id_base);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if (valid && dist[i] < thr_r[i]) B.append(acc_row(i, lane), (float)dist[i], id);
+        for (int i = 0; i < F::kND; ++i) {
+          if (valid[F::block(i)] && dist[i] < thr_r[F::slot(i)])
+            B.append(F::row(F::slot(i), lane), (float)dist[i], id + QB * F::block(i));
         }
         wave_sync();
         if (B.maybe_compact()) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int m = acc_row(i, lane);
+          for (int r = 0; r < F::kNR; ++r) {
+            const int m = F::row(r, lane);
             const float t = B.thr[m];
-            if (q0 + m < nq) thr_r[i] = t == INFINITY ? INT32_MAX : (int32_t)t;
+            if (q0 + m < nq) thr_r[r] = t == INFINITY ? INT32_MAX : (int32_t)t;
           }
         }
       }
@@ -298,7 +359,7 @@ __global__ __launch_bounds__(64) void knn_f32_kernel(const float* __restrict__ x
   const int q0 = blockIdx.x * kQB;
   const int64_t slice = blockIdx.y;
   const int64_t start = slice * slice_len, end = min(n, start + slice_len);
-  KnnBuf B = knn_buf(smem_raw, k);
+  KnnBuf<kQB> B = knn_buf<kQB>(smem_raw, k);
   float* qt = reinterpret_cast<float*>(B.thr + kQB);
   for (int e = lane; e < kQB * dim; e += kWave) {
     const int m = e / dim;
@@ -383,7 +444,7 @@ __global__ __launch_bounds__(64) void knn_merge_kernel(float* __restrict__ part_
   }
 }
 
-size_t knn_buf_bytes(int k) { return (size_t)kQB * (k + 64) * 8 + (size_t)kQB * 8; }
+size_t knn_buf_bytes(int qb, int k) { return (size_t)qb * (k + 64) * 8 + (size_t)qb * 8; }
 
 }  // namespace
 
@@ -401,10 +462,8 @@ hipError_t launch_knn_merge(float* part_d, int32_t* part_i, int nq, int k, int64
   return hipSuccess;
 }
 
-int knn_queries_per_block() { return kQB; }
-
-size_t knn_smem_bytes(int dtype, int dim, int k) {
-  return knn_buf_bytes(k) + (dtype == 0 ? 0 : (size_t)kQB * dim * 4);
+size_t knn_smem_bytes(int dtype, int qb, int dim, int k) {
+  return dtype == 0 ? knn_buf_bytes(qb, k) : knn_buf_bytes(kQB, k) + (size_t)kQB * dim * 4;
 }
 
 hipError_t launch_knn_prep_u8(const uint8_t* x, int64_t n, int dim, int dp, int8_t* xs, int32_t* xn,
@@ -425,37 +484,80 @@ hipError_t launch_knn_prep_u8(const uint8_t* x, int64_t n, int dim, int dp, int8
   return hipGetLastError();
 }
 
-hipError_t launch_knn_u8(const int8_t* xs, const int32_t* xn, int64_t n, int dp, const int8_t* qs,
-                         const int32_t* qn, int nq, int k, int64_t slices, int64_t slice_len,
-                         int64_t id_base, float* part_d, int32_t* part_i, hipStream_t stream) {
-  const dim3 grid((unsigned)((nq + kQB - 1) / kQB), (unsigned)slices);
-  const size_t smem = knn_smem_bytes(0, dp, k);
-  switch (dp / 32) {
-#define GANN_KNN_CASE(S)                                                                      \
-  case S:                                                                                     \
-    hipLaunchKernelGGL(knn_u8_kernel<S>, grid, dim3(64), smem, stream, xs, xn, n, qs, qn, nq, \
-                       k, slice_len, id_base, part_d, part_i);                                \
-    break;
-    GANN_KNN_CASE(1)
-    GANN_KNN_CASE(2)
-    GANN_KNN_CASE(3)
-    GANN_KNN_CASE(4)
-    GANN_KNN_CASE(5)
-    GANN_KNN_CASE(6)
-    GANN_KNN_CASE(7)
-    GANN_KNN_CASE(8)
-#undef GANN_KNN_CASE
-    default:
-      return hipErrorInvalidValue;
+namespace {
+
+// Calls f with the uint8 kernel of QB queries for rows of dp bytes (a
+// multiple of 1024 / QB, at most 256).
+template <int QB, typename F>
+hipError_t with_knn_u8_kernel(int dp, F f) {
+  constexpr int kK = U8Form<QB, 1>::kK;
+  if (dp % kK != 0) return hipErrorInvalidValue;
+  switch (dp / kK) {
+    case 1: return f(knn_u8_kernel<QB, 1>);
+    case 2: return f(knn_u8_kernel<QB, 2>);
+    case 3: return f(knn_u8_kernel<QB, 3>);
+    case 4: return f(knn_u8_kernel<QB, 4>);
+    default: break;
   }
-  return hipGetLastError();
+  if constexpr (QB == 32) {
+    switch (dp / kK) {
+      case 5: return f(knn_u8_kernel<QB, 5>);
+      case 6: return f(knn_u8_kernel<QB, 6>);
+      case 7: return f(knn_u8_kernel<QB, 7>);
+      case 8: return f(knn_u8_kernel<QB, 8>);
+      default: break;
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int QB>
+int u8_blocks_per_cu(int dp, int k) {
+  int nb = 0;
+  const size_t smem = knn_smem_bytes(0, QB, dp, k);
+  const hipError_t e = with_knn_u8_kernel<QB>(dp, [&](auto kern) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, kWave, smem);
+  });
+  return e == hipSuccess ? nb : 0;
+}
+
+}  // namespace
+
+KnnU8Form knn_u8_form(int dim, int k) {
+  KnnU8Form f32{32, (dim + 31) / 32 * 32, 0}, f16{16, (dim + 63) / 64 * 64, 0};
+  f32.blocks_per_cu = u8_blocks_per_cu<32>(f32.dp, k);
+  f16.blocks_per_cu = u8_blocks_per_cu<16>(f16.dp, k);
+  return 16 * f16.blocks_per_cu > 32 * f32.blocks_per_cu ? f16 : f32;
+}
+
+int knn_f32_blocks_per_cu(int dim, int k) {
+  int nb = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, knn_f32_kernel, kWave,
+                                                                   knn_smem_bytes(1, kQB, dim, k));
+  return e == hipSuccess ? nb : 0;
+}
+
+hipError_t launch_knn_u8(const KnnU8Form& form, const int8_t* xs, const int32_t* xn, int64_t n,
+                         const int8_t* qs, const int32_t* qn, int nq, int k, int64_t slices,
+                         int64_t slice_len, int64_t id_base, float* part_d, int32_t* part_i,
+                         hipStream_t stream) {
+  const dim3 grid((unsigned)((nq + form.qb - 1) / form.qb), (unsigned)slices);
+  const size_t smem = knn_smem_bytes(0, form.qb, form.dp, k);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(kWave), smem, stream, xs, xn, n, qs, qn, nq, k, slice_len,
+                       id_base, part_d, part_i);
+    return hipGetLastError();
+  };
+  if (form.qb == 32) return with_knn_u8_kernel<32>(form.dp, go);
+  if (form.qb == 16) return with_knn_u8_kernel<16>(form.dp, go);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_knn_f32(const float* x, int64_t n, int dim, const float* q, int nq, int k,
                           int64_t slices, int64_t slice_len, int64_t id_base, float* part_d,
                           int32_t* part_i, hipStream_t stream) {
   const dim3 grid((unsigned)((nq + kQB - 1) / kQB), (unsigned)slices);
-  hipLaunchKernelGGL(knn_f32_kernel, grid, dim3(64), knn_smem_bytes(1, dim, k), stream, x, n, dim,
+  hipLaunchKernelGGL(knn_f32_kernel, grid, dim3(64), knn_smem_bytes(1, kQB, dim, k), stream, x, n, dim,
                      q, nq, k, slice_len, id_base, part_d, part_i);
   return hipGetLastError();
 }
