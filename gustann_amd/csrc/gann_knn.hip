@@ -49,13 +49,15 @@ __device__ __forceinline__ uint64_t cand_key(float d, int32_t id) {
 }
 
 // Per-wavefront candidate buffers of QB queries: query m keeps keys
-// [0, cnt[m]) of bk[m * cap ...]; thr[m] is the k-th smallest kept distance
-// once k are kept (+inf before).  cap = k + 64 >= k + one tile.
+// [0, cnt[m]) of bk[m * cap ...], of which the first srt[m] (those kept by
+// the last cut) are sorted; thr[m] is the k-th smallest kept distance once k
+// are kept (+inf before).  cap = k + 64 >= k + one tile.
 template <int QB>
 struct KnnBuf {
   uint64_t* bk;
   int32_t* cnt;
   float* thr;
+  int32_t* srt;
   int cap, k;
 
   __device__ void init() {
@@ -63,6 +65,7 @@ struct KnnBuf {
     if (lane < QB) {
       cnt[lane] = 0;
       thr[lane] = INFINITY;
+      srt[lane] = 0;
     }
     wave_sync();
   }
@@ -72,12 +75,45 @@ struct KnnBuf {
     bk[(size_t)m * cap + slot] = cand_key(d, id);
   }
 
-  // Keeps the k smallest keys of query m, sorted (each key's rank is the
-  // number of smaller keys).
+  // Keeps the k smallest keys of query m, sorted.  The keys are distinct
+  // (one per point).  With a sorted prefix of h and at most 64 keys after it
+  // (every cut but a query's first), a merge: new key x goes to
+  // #{new < x} + #{old < x}, old key i to i + #{new < old i}; the counts over
+  // the new keys come from one pass over them, #{old < x} from a binary
+  // search of the prefix.  Otherwise each key goes to its rank among all.
   __device__ void compact(int m) {
     const int lane = lane_id();
-    const int n = cnt[m];
+    const int n = cnt[m], h = srt[m], nn = n - h;
     uint64_t* k_m = bk + (size_t)m * cap;
+    if (h > 0 && nn <= kWave) {
+      const uint64_t x = lane < nn ? k_m[h + lane] : ~(uint64_t)0;
+      const uint64_t o0 = lane < h ? k_m[lane] : ~(uint64_t)0;
+      const uint64_t o1 = lane + kWave < h ? k_m[lane + kWave] : ~(uint64_t)0;
+      int rn = 0, c0 = 0, c1 = 0;
+#pragma unroll 8
+      for (int j = 0; j < nn; ++j) {
+        const uint64_t w = k_m[h + j];
+        rn += w < x ? 1 : 0;
+        c0 += w < o0 ? 1 : 0;
+        c1 += w < o1 ? 1 : 0;
+      }
+      int lo = 0, hi = h;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (k_m[mid] < x) lo = mid + 1; else hi = mid;
+      }
+      wave_sync();
+      if (lane < nn && rn + lo < k) k_m[rn + lo] = x;
+      if (lane < h && lane + c0 < k) k_m[lane + c0] = o0;
+      if (lane + kWave < h && lane + kWave + c1 < k) k_m[lane + kWave + c1] = o1;
+      wave_sync();
+      if (lane == 0) {
+        cnt[m] = srt[m] = min(n, k);
+        thr[m] = n >= k ? __uint_as_float((uint32_t)(k_m[k - 1] >> 32)) : INFINITY;
+      }
+      wave_sync();
+      return;
+    }
     uint64_t v[3];
     int rk[3];
 #pragma unroll
@@ -100,7 +136,7 @@ struct KnnBuf {
     }
     wave_sync();
     if (lane == 0) {
-      cnt[m] = min(n, k);
+      cnt[m] = srt[m] = min(n, k);
       thr[m] = n >= k ? __uint_as_float((uint32_t)(k_m[k - 1] >> 32)) : INFINITY;
     }
     wave_sync();
@@ -143,6 +179,7 @@ __device__ __forceinline__ KnnBuf<QB> knn_buf(uint8_t* smem, int k) {
   B.bk = reinterpret_cast<uint64_t*>(smem);
   B.cnt = reinterpret_cast<int32_t*>(B.bk + (size_t)QB * B.cap);
   B.thr = reinterpret_cast<float*>(B.cnt + QB);
+  B.srt = B.cnt + 2 * QB;
   return B;
 }
 
@@ -360,7 +397,7 @@ __global__ __launch_bounds__(64) void knn_f32_kernel(const float* __restrict__ x
   const int64_t slice = blockIdx.y;
   const int64_t start = slice * slice_len, end = min(n, start + slice_len);
   KnnBuf<kQB> B = knn_buf<kQB>(smem_raw, k);
-  float* qt = reinterpret_cast<float*>(B.thr + kQB);
+  float* qt = reinterpret_cast<float*>(B.srt + kQB);
   for (int e = lane; e < kQB * dim; e += kWave) {
     const int m = e / dim;
     qt[e] = q0 + m < nq ? q[(size_t)(q0 + m) * dim + (e - m * dim)] : 0.0f;
@@ -444,7 +481,7 @@ __global__ __launch_bounds__(64) void knn_merge_kernel(float* __restrict__ part_
   }
 }
 
-size_t knn_buf_bytes(int qb, int k) { return (size_t)qb * (k + 64) * 8 + (size_t)qb * 8; }
+size_t knn_buf_bytes(int qb, int k) { return (size_t)qb * (k + 64) * 8 + (size_t)qb * 12; }
 
 }  // namespace
 

@@ -55,3 +55,31 @@ def test_tree_merge_is_the_k_smallest(k):
         got = merge_tree(slots, k)
         want = sorted(every)[:k]
         assert got == want + [PAD] * (k - len(want)), (k, trial, nslots)
+
+
+def compact_merge(buf, h, k):
+    """knn_u8/f32 kernels' KnnBuf::compact, merge path (gann_knn.hip): the
+    sorted prefix buf[:h] and at most 64 new keys buf[h:]; new key x goes to
+    #{new < x} + #{old < x}, old key i to i + #{new < old i}; kept below k."""
+    old, new = buf[:h], buf[h:]
+    out = [None] * min(len(buf), k)
+    for x in new:
+        p = sum(1 for w in new if w < x) + bisect.bisect_left(old, x)
+        if p < k:
+            out[p] = x
+    for i, o in enumerate(old):
+        p = i + sum(1 for w in new if w < o)
+        if p < k:
+            out[p] = o
+    return out
+
+
+@pytest.mark.parametrize("k", [1, 2, 10, 64, 100, 128])
+def test_compaction_merge_keeps_the_k_smallest(k):
+    rng = random.Random(100 + k)
+    for trial in range(300):
+        h = rng.randrange(1, k + 1)                 # the kept, sorted prefix
+        nn = rng.randrange(0, 65)                   # new keys since the last cut
+        keys = rng.sample(range(1 << 40), h + nn)   # distinct, as (dist, id) keys are
+        buf = sorted(keys[:h]) + keys[h:]
+        assert compact_merge(buf, h, k) == sorted(keys)[:k], (k, trial)
