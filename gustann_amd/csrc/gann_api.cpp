@@ -265,6 +265,7 @@ struct gann_handle {
   gann::NavDev nav{};
   // per-call scratch
   DevBuf q, entries, local, nns, dists, found, nexp, nadc, counters, qs;
+  DevBuf entry_dist, order;  // the fused kernels' query order (run_entries)
   DevBuf luts, lists, state;
   PinnedBuf counter_host;
   // this device's copy of the fixed scratch of gann_search_device_noalloc
@@ -772,7 +773,25 @@ struct SearchScratch {
     h->qs.ensure((size_t)nfloats * 4);
     return h->qs.as<float>();
   }
+  const int32_t* query_order = nullptr;  // set by order_queries for this call
 };
+
+// The order in which the fused kernels take the queries of this call:
+// farthest from its entry point first (query_order_kernel in
+// gann_kernels.hip).  Not in the allocation-free calls, which keep the
+// queue's order; GANN_QUERY_ORDER=0 keeps it too.  Results are the same
+// either way.
+void order_queries(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t nq, const int32_t* entries,
+                   hipStream_t s) {
+  sc.query_order = nullptr;
+  const char* e = std::getenv("GANN_QUERY_ORDER");
+  if (sc.fixed() || (e && std::atoi(e) == 0)) return;
+  h->entry_dist.ensure((size_t)nq * 4);
+  h->order.ensure((size_t)nq * 4);
+  GANN_HIP(gann::launch_query_order(h->ix, h->dtype, q_dev, nq, entries, h->entry_dist.as<float>(),
+                                    h->order.as<int32_t>(), s));
+  sc.query_order = h->order.as<int32_t>();
+}
 
 void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t nq, int32_t topk,
                 int32_t L, int32_t mode, const int32_t* entries, int32_t* nns, float* dists,
@@ -795,8 +814,10 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
     int32_t* ctr = sc.counters();
     float* qs = sc.qs((int64_t)nq * Ly.dim);
     const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
+    order_queries(h, sc, q_dev, nq, entries, s);
     GANN_HIP(gann::launch_search_beam(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, beam,
-                                      nns, dists, found, nexp, nadc, ctr + 2, qs, waves, blocks, gp, s));
+                                      nns, dists, found, nexp, nadc, ctr + 2, sc.query_order, qs, waves,
+                                      blocks, gp, s));
     return;
   }
   if (mode == GANN_MODE_FUSED || mode == GANN_MODE_FUSED_GP) {
@@ -871,9 +892,10 @@ void run_search(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_t n
       int32_t* ctr = sc.counters();
       float* qs = sc.qs((int64_t)nq * Ly.dim);
       const int blocks = std::max(1, std::min(h->num_cus, (nq + waves - 1) / waves));
+      order_queries(h, sc, q_dev, nq, entries, s);
       GANN_HIP(gann::launch_search_cb(h->ix, h->pq.dev, h->dtype, q_dev, nq, entries, topk, L, nns,
-                                      dists, found, nexp, nadc, ctr + 2, qs, waves, blocks, gp,
-                                      gp ? g : 0, s));
+                                      dists, found, nexp, nadc, ctr + 2, sc.query_order, qs, waves,
+                                      blocks, gp, gp ? g : 0, s));
       return;
     }
     if (mode == GANN_MODE_FUSED_GP)

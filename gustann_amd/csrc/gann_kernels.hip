@@ -207,6 +207,70 @@ __global__ __launch_bounds__(64) void nav_entry_kernel(NavDev nav, int64_t medoi
   }
 }
 
+// Squared distance of each query to its entry point (the order key of
+// query_order_kernel); entries outside the index give 0.
+template <typename T>
+__global__ void entry_dist_kernel(IndexDev ix, const float* __restrict__ q, int nq,
+                                  const int32_t* __restrict__ entries, float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nq) return;
+  const int32_t u = entries[i];
+  float s = 0.0f;
+  if (u >= 0 && u < ix.num_pts) {
+    const T* x = reinterpret_cast<const T*>(record_of(ix, u));
+    const float* qq = q + (int64_t)i * ix.dim;
+    for (int d = 0; d < ix.dim; ++d) {
+      const float t = qq[d] - to_f(x[d]);
+      s = fma_f(t, t, s);
+    }
+  }
+  out[i] = s;
+}
+
+// The order in which the persistent search kernels take the queries: the
+// farthest from its entry point first.  Expansions per query vary (2,577 to
+// 6,994 at L = 2576 on a 100M mixture, mean 3,044) and grow with that
+// distance, so long searches start early and the last queries taken are
+// short ones, instead of a long one holding the kernel open while most lists
+// are idle.  A counting sort on 4096 buckets of the distance's bit pattern
+// (a non-negative float's bits order like its value; exponent and 4
+// mantissa bits), in one workgroup; order within a bucket is arbitrary.  No
+// result depends on the order: each query's search is independent.
+constexpr int kOrderBuckets = 4096, kOrderThreads = 1024;
+
+__device__ __forceinline__ int order_bucket(float d) {
+  const uint32_t b = __float_as_uint(d) >> 19;
+  return kOrderBuckets - 1 - (int)min(b, (uint32_t)(kOrderBuckets - 1));
+}
+
+__global__ __launch_bounds__(kOrderThreads) void query_order_kernel(const float* __restrict__ d, int nq,
+                                                                    int32_t* __restrict__ order) {
+  __shared__ int cnt[kOrderBuckets];
+  __shared__ int wave_sum[kOrderThreads / kWave];
+  constexpr int kPer = kOrderBuckets / kOrderThreads;
+  const int t = threadIdx.x, wave = t / kWave;
+  for (int b = t; b < kOrderBuckets; b += kOrderThreads) cnt[b] = 0;
+  __syncthreads();
+  for (int i = t; i < nq; i += kOrderThreads) atomicAdd(&cnt[order_bucket(d[i])], 1);
+  __syncthreads();
+  // exclusive scan of the counts: thread t owns buckets kPer t .. kPer t + kPer - 1
+  int c[kPer], s = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) s += (c[j] = cnt[kPer * t + j]);
+  const int incl = wave_incl_scan(s);
+  if (lane_id() == kWave - 1) wave_sum[wave] = incl;
+  __syncthreads();
+  int off = incl - s;
+  for (int w = 0; w < wave; ++w) off += wave_sum[w];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    cnt[kPer * t + j] = off;
+    off += c[j];
+  }
+  __syncthreads();
+  for (int i = t; i < nq; i += kOrderThreads) order[atomicAdd(&cnt[order_bucket(d[i])], 1)] = i;
+}
+
 // q - mu of every query (src/impl/pq.cuh:22-24), read back with uniform
 // (scalar) loads by the shared-codebook ADC.
 __global__ void query_centre_kernel(const float* __restrict__ q, const float* __restrict__ centroid,
@@ -345,6 +409,20 @@ hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_
   return hipGetLastError();
 }
 
+hipError_t launch_query_order(const IndexDev& ix, int dtype, const float* q, int nq, const int32_t* entries,
+                              float* entry_dist, int32_t* order, hipStream_t stream) {
+  if (nq <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((nq + 255) / 256));
+  if (dtype == 0)
+    hipLaunchKernelGGL(entry_dist_kernel<uint8_t>, grid, dim3(256), 0, stream, ix, q, nq, entries, entry_dist);
+  else
+    hipLaunchKernelGGL(entry_dist_kernel<float>, grid, dim3(256), 0, stream, ix, q, nq, entries, entry_dist);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(query_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, entry_dist, nq, order);
+  return hipGetLastError();
+}
+
 hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                          const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                          int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream) {
@@ -405,7 +483,7 @@ hipError_t prepare_cb(const IndexDev& ix, const PQDev& pq, const float* q, int n
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                            float* qs_all, int waves, int blocks, bool global_pivots, int lds_groups,
+                            const int32_t* order, float* qs_all, int waves, int blocks, bool global_pivots, int lds_groups,
                             hipStream_t stream) {
   if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
   const int split = search_cb_split_groups(pq.M, pq.chunk_w);
@@ -421,16 +499,16 @@ hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, cons
   hipError_t e = prepare_cb(ix, pq, q, nq, queue, qs_all, stream);
   if (e != hipSuccess) return e;
   if (dtype == 0)
-    return launch_search_cb_u8(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all,
+    return launch_search_cb_u8(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order, qs_all,
                                waves, blocks, global_pivots, lds_groups, smem, stream);
-  return launch_search_cb_f32(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all,
+  return launch_search_cb_f32(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order, qs_all,
                               waves, blocks, global_pivots, lds_groups, smem, stream);
 }
 
 hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                               const int32_t* entries, int topk, int L, int bw, int32_t* nns,
                               float* dists, int32_t* found, int32_t* n_exp, int32_t* n_adc,
-                              int32_t* queue, float* qs_all, int waves, int blocks,
+                              int32_t* queue, const int32_t* order, float* qs_all, int waves, int blocks,
                               bool global_pivots, hipStream_t stream) {
   if (bw < 2 || bw > kMaxBeam) return hipErrorInvalidValue;
   if (global_pivots && !pq.piv_cb) return hipErrorInvalidValue;
@@ -439,9 +517,9 @@ hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, co
   hipError_t e = prepare_cb(ix, pq, q, nq, queue, qs_all, stream);
   if (e != hipSuccess) return e;
   if (dtype == 0)
-    return launch_search_beam_u8(ix, pq, q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue,
+    return launch_search_beam_u8(ix, pq, q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue, order,
                                  qs_all, waves, blocks, global_pivots, smem, stream);
-  return launch_search_beam_f32(ix, pq, q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue,
+  return launch_search_beam_f32(ix, pq, q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue, order,
                                 qs_all, waves, blocks, global_pivots, smem, stream);
 }
 

@@ -26,6 +26,11 @@ hipError_t launch_pq_adc_scan(const PQDev& pq, const float* q, int nq, const int
 hipError_t launch_nav_entry(const NavDev& nav, int dtype, int64_t medoid, int64_t num_pts, int dim,
                             const float* q, int nq, int32_t* entries, int32_t* local_out,
                             int32_t* fallback_count, hipStream_t stream);
+// order[0..nq): the queries by their squared distance to their entry point
+// (into entry_dist[nq]), largest first (approximately: 4096 buckets), the
+// order in which the fused search kernels take them.
+hipError_t launch_query_order(const IndexDev& ix, int dtype, const float* q, int nq, const int32_t* entries,
+                              float* entry_dist, int32_t* order, hipStream_t stream);
 hipError_t launch_search(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                          const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                          int32_t* found, int32_t* n_exp, int32_t* n_adc, hipStream_t stream);
@@ -67,14 +72,14 @@ void search_cb_pivot_layout(const float* pivots, int dim, uint8_t* out);
 hipError_t launch_search_cb(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                             const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                             int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                            float* qs_all, int waves, int blocks, bool global_pivots,
+                            const int32_t* order, float* qs_all, int waves, int blocks, bool global_pivots,
                             int lds_groups, hipStream_t stream);
 // Beam search with beam width bw in [2, max_beam_width()] (same LDS layout,
 // pivot placement and launch shape as launch_search_cb).
 hipError_t launch_search_beam(const IndexDev& ix, const PQDev& pq, int dtype, const float* q, int nq,
                               const int32_t* entries, int topk, int L, int bw, int32_t* nns,
                               float* dists, int32_t* found, int32_t* n_exp, int32_t* n_adc,
-                              int32_t* queue, float* qs_all, int waves, int blocks,
+                              int32_t* queue, const int32_t* order, float* qs_all, int waves, int blocks,
                               bool global_pivots, hipStream_t stream);
 int max_beam_width();
 hipError_t launch_step_init(const PQDev& pq, const float* q, int nq, const int32_t* entries,

@@ -482,7 +482,7 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
     IndexDev ix, PQDev pq, const float* __restrict__ q, int nq, const int32_t* __restrict__ entries,
     int topk, int L, int32_t* __restrict__ nns, float* __restrict__ dists,
     int32_t* __restrict__ found_cnt, int32_t* __restrict__ n_exp, int32_t* __restrict__ n_adc,
-    int32_t* __restrict__ queue, const float* __restrict__ qs_all) {
+    int32_t* __restrict__ queue, const int32_t* __restrict__ order, const float* __restrict__ qs_all) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
   const uint32_t rowb = cb_stride(4 * dim);
@@ -537,6 +537,7 @@ __global__ __launch_bounds__(cb_block_threads(KP, kSplitG)) void search_cb_kerne
     if (lane == 0) qi = atomicAdd(queue, 1);
     qi = __builtin_amdgcn_readfirstlane(__shfl(qi, 0, kWave));
     if (qi >= nq) break;
+    if (order) qi = __builtin_amdgcn_readfirstlane(order[qi]);  // queue position -> query
     int32_t u = __builtin_amdgcn_readfirstlane(entries[qi]);
     if (u >= ix.num_pts) u = -1;  // caller-given entries outside the index: empty result
     RecRegs<T, KP, NB> cur;
@@ -672,7 +673,7 @@ __global__ __launch_bounds__(cb_block_threads(KP)) void search_beam_kernel(
     IndexDev ix, PQDev pq, const float* __restrict__ q, int nq, const int32_t* __restrict__ entries,
     int topk, int L, int bw, int32_t* __restrict__ nns, float* __restrict__ dists,
     int32_t* __restrict__ found_cnt, int32_t* __restrict__ n_exp, int32_t* __restrict__ n_adc,
-    int32_t* __restrict__ queue, const float* __restrict__ qs_all) {
+    int32_t* __restrict__ queue, const int32_t* __restrict__ order, const float* __restrict__ qs_all) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   const int dim = ix.dim, M = pq.M, R = ix.R;
   const uint32_t rowb = cb_stride(4 * dim);
@@ -704,6 +705,7 @@ __global__ __launch_bounds__(cb_block_threads(KP)) void search_beam_kernel(
     if (lane == 0) qi = atomicAdd(queue, 1);
     qi = __builtin_amdgcn_readfirstlane(__shfl(qi, 0, kWave));
     if (qi >= nq) break;
+    if (order) qi = __builtin_amdgcn_readfirstlane(order[qi]);  // queue position -> query
     const float* qq = q + (int64_t)qi * dim;
     const float* qs = qs_all + (int64_t)qi * dim;
     float qv[KP];
@@ -957,7 +959,7 @@ template <typename T>
 hipError_t launch_search_cb_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
                               const int32_t* entries, int topk, int L, int32_t* nns, float* dists,
                               int32_t* found, int32_t* n_exp, int32_t* n_adc, int32_t* queue,
-                              const float* qs_all, int waves, int blocks, bool global_pivots,
+                              const int32_t* order, const float* qs_all, int waves, int blocks, bool global_pivots,
                               int lds_groups, size_t smem, hipStream_t stream) {
   return with_nb(ix.R, [&](auto nb) {
     constexpr int NBv = decltype(nb)::value;
@@ -978,7 +980,7 @@ hipError_t launch_search_cb_t(const IndexDev& ix, const PQDev& pq, const float* 
             constexpr int kG = decltype(g)::value;
             return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kG, KPv, NBv>, [&] {
               hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kG, KPv, NBv>), grid, block, smem, stream,
-                                 ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+                                 ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order, qs_all);
             });
           };
           if (lds_groups == kGpWide) return wide(ic<kGpWide>{});
@@ -995,23 +997,23 @@ hipError_t launch_search_cb_t(const IndexDev& ix, const PQDev& pq, const float* 
         if (global_pivots && lds_groups > 0 && lds_groups == kSplit)
           return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kSplit, KPv, NBv>, [&] {
             hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kSplit, KPv, NBv>), grid, block, smem, stream,
-                               ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+                               ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order, qs_all);
           });
         if (global_pivots && lds_groups > 0 && lds_groups == kHalf)
           return launch_checked(&search_cb_kernel<T, MWv, Wv, true, kHalf, KPv, NBv>, [&] {
             hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, kHalf, KPv, NBv>), grid, block, smem, stream,
-                               ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+                               ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order, qs_all);
           });
       }
       if (lds_groups != 0) return hipErrorInvalidValue;
       if (global_pivots)
         return launch_checked(&search_cb_kernel<T, MWv, Wv, true, 0, KPv, NBv>, [&] {
           hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, true, 0, KPv, NBv>), grid, block, smem, stream, ix,
-                             pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+                             pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order, qs_all);
         });
       return launch_checked(&search_cb_kernel<T, MWv, Wv, false, 0, KPv, NBv>, [&] {
         hipLaunchKernelGGL((search_cb_kernel<T, MWv, Wv, false, 0, KPv, NBv>), grid, block, smem, stream, ix,
-                           pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, qs_all);
+                           pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order, qs_all);
       });
     });
   });
@@ -1021,7 +1023,7 @@ template <typename T>
 hipError_t launch_search_beam_t(const IndexDev& ix, const PQDev& pq, const float* q, int nq,
                                 const int32_t* entries, int topk, int L, int bw, int32_t* nns,
                                 float* dists, int32_t* found, int32_t* n_exp, int32_t* n_adc,
-                                int32_t* queue, const float* qs_all, int waves, int blocks,
+                                int32_t* queue, const int32_t* order, const float* qs_all, int waves, int blocks,
                                 bool global_pivots, size_t smem, hipStream_t stream) {
   return with_nb(ix.R, [&](auto nb) {
     constexpr int NBv = decltype(nb)::value;
@@ -1032,11 +1034,11 @@ hipError_t launch_search_beam_t(const IndexDev& ix, const PQDev& pq, const float
       if (global_pivots)
         return launch_checked(&search_beam_kernel<T, MWv, Wv, KPv, true, NBv>, [&] {
           hipLaunchKernelGGL((search_beam_kernel<T, MWv, Wv, KPv, true, NBv>), grid, block, smem, stream, ix, pq,
-                             q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue, qs_all);
+                             q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue, order, qs_all);
         });
       return launch_checked(&search_beam_kernel<T, MWv, Wv, KPv, false, NBv>, [&] {
         hipLaunchKernelGGL((search_beam_kernel<T, MWv, Wv, KPv, false, NBv>), grid, block, smem, stream, ix, pq,
-                           q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue, qs_all);
+                           q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc, queue, order, qs_all);
       });
     });
   });
@@ -1083,12 +1085,12 @@ namespace gann {
 #define GANN_CB_ARGS                                                                                \
   const IndexDev &ix, const PQDev &pq, const float *q, int nq, const int32_t *entries, int topk,     \
       int L, int32_t *nns, float *dists, int32_t *found, int32_t *n_exp, int32_t *n_adc,             \
-      int32_t *queue, const float *qs_all, int waves, int blocks, bool global_pivots, int lds_groups, \
+      int32_t *queue, const int32_t *order, const float *qs_all, int waves, int blocks, bool global_pivots, int lds_groups, \
       size_t smem, hipStream_t stream
 #define GANN_BEAM_ARGS                                                                              \
   const IndexDev &ix, const PQDev &pq, const float *q, int nq, const int32_t *entries, int topk,     \
       int L, int bw, int32_t *nns, float *dists, int32_t *found, int32_t *n_exp, int32_t *n_adc,     \
-      int32_t *queue, const float *qs_all, int waves, int blocks, bool global_pivots, size_t smem,   \
+      int32_t *queue, const int32_t *order, const float *qs_all, int waves, int blocks, bool global_pivots, size_t smem,   \
       hipStream_t stream
 #define GANN_LUT_ARGS                                                                               \
   const IndexDev &ix, const PQDev &pq, const float *q, int nq, const int32_t *entries, int topk,     \

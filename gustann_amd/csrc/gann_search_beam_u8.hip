@@ -6,7 +6,7 @@ namespace gann {
 
 hipError_t launch_search_beam_u8(GANN_BEAM_ARGS) {
   return launch_search_beam_t<uint8_t>(ix, pq, q, nq, entries, topk, L, bw, nns, dists, found, n_exp, n_adc,
-                                  queue, qs_all, waves, blocks, global_pivots, smem, stream);
+                                  queue, order, qs_all, waves, blocks, global_pivots, smem, stream);
 }
 
 }  // namespace gann

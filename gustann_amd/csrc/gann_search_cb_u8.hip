@@ -5,7 +5,7 @@
 namespace gann {
 
 hipError_t launch_search_cb_u8(GANN_CB_ARGS) {
-  return launch_search_cb_t<uint8_t>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue,
+  return launch_search_cb_t<uint8_t>(ix, pq, q, nq, entries, topk, L, nns, dists, found, n_exp, n_adc, queue, order,
                                 qs_all, waves, blocks, global_pivots, lds_groups, smem, stream);
 }
 

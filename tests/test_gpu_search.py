@@ -299,6 +299,26 @@ def test_pivot_table_forms_match_oracle(u8, form, monkeypatch):
         _assert_same(got, (on, od, of), ne, oe)
 
 
+@pytest.mark.parametrize("mode,bw", [(MODE_FUSED, 1), (MODE_FUSED_GP, 1), (MODE_FUSED, 3)])
+def test_query_order_changes_no_result(u8, monkeypatch, mode, bw):
+    # with a pivot graph the fused kernels take the queries farthest from
+    # their entry first (GANN_QUERY_ORDER=0: in queue order); every output
+    # stays the same and equal to the oracle's (beam width 1)
+    meta, g, ix = u8
+    Q = _queries(meta)
+    Q = np.concatenate([Q, Q[::-1], Q[::2]])
+    runs = []
+    for env in ("1", "0"):
+        monkeypatch.setenv("GANN_QUERY_ORDER", env)
+        ne = np.empty(Q.shape[0], np.int32)
+        got = g.search(Q, Q.shape[0], 10, 64, beam_width=bw, mode=mode, n_exp=ne)
+        runs.append((got, ne))
+    _assert_same(runs[0][0], runs[1][0], runs[0][1], runs[1][1])
+    if bw == 1:
+        on, od, of, oe, _ = ix.search(Q, 10, 64, threads=8)
+        _assert_same(runs[0][0], (on, od, of), runs[0][1], oe)
+
+
 @pytest.mark.parametrize("dtype,D,M,R", [("uint8", 32, 16, 64), ("uint8", 64, 16, 40), ("uint8", 64, 32, 64),
                                          ("float", 96, 48, 64), ("uint8", 128, 64, 48), ("uint8", 128, 32, 100)])
 def test_wide_lookup_form_matches_oracle(tmp_path, monkeypatch, dtype, D, M, R):
