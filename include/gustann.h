@@ -136,10 +136,12 @@ int gann_search_ex(gann_handle* h, const float* q, int32_t nq, int32_t topk, int
  * enqueued on `stream` (a hipStream_t; 0 = the default stream).
  * entries_dev: [nq] device scratch for the entry ids.  n_exp_dev/n_adc_dev
  * nullable [nq].  The kernels also use scratch owned by the handle (the
- * query queue counter, q - centroid of every query, and the step-wise
- * modes' LUTs, lists and states), so at most one call per handle may be in
- * flight: a caller that enqueues calls of one handle on different streams
- * orders them itself (or uses one handle per stream). */
+ * query queue counter, q - centroid of every query, the order in which the
+ * fused kernels take the queries, and the step-wise modes' LUTs, lists and
+ * states), so at most one call per handle may be in flight: a caller that
+ * enqueues calls of one handle on different streams orders them itself (or
+ * uses one handle per stream).  The fused kernels take the queries farthest
+ * from their entry point first; every result is the same in any order. */
 int gann_search_device(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                        int32_t* entries_dev, int32_t* nns_dev, float* dists_dev,
                        int32_t* found_dev, int32_t* n_exp_dev, int32_t* n_adc_dev, void* stream);
@@ -162,7 +164,9 @@ int gann_search_device_ex(gann_handle* h, const float* q_dev, int32_t nq, int32_
  * (GANN_MODE_FUSED, GANN_MODE_FUSED_GP, GANN_MODE_FUSED_LUT; the step-wise
  * modes return GANN_ERR_UNSUPPORTED).  Every call on one GPU shares that
  * array, whichever handle it comes from: calls that overlap on one GPU race,
- * so the caller orders them.  Arguments and results as gann_search_device_ex. */
+ * so the caller orders them.  Arguments and results as gann_search_device_ex
+ * (the queries are taken in queue order: the fixed array holds no order,
+ * which changes the time, not the results). */
 int gann_search_device_noalloc(gann_handle* h, const float* q_dev, int32_t nq, int32_t topk, int32_t L,
                                int32_t beam_width, int32_t mode, int32_t* entries_dev, int32_t* nns_dev,
                                float* dists_dev, int32_t* found_dev, int32_t* n_exp_dev,
