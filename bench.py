@@ -295,6 +295,8 @@ def bench_c3(args):
                    "L": L, "recall_at_10": rec10, "recall_queries": int(gt.shape[0]),
                    "expansions_per_query": exps / ds.nq, "L_sweep": sweep,
                    "search_kernel_ms": ms_k, "entry_selection_ms": ms - ms_k,
+                   "query_order": ("queue order" if os.environ.get("GANN_QUERY_ORDER", "1").strip() == "0"
+                                   else "farthest from the entry point first"),
                    "dataset_build_s": meta.get("build_s") if build_s > 60 else None,
                    "dataset_ready_s": build_s, "timed_wall_s": wall},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -785,7 +785,7 @@ void order_queries(gann_handle* h, SearchScratch& sc, const float* q_dev, int32_
                    hipStream_t s) {
   sc.query_order = nullptr;
   const char* e = std::getenv("GANN_QUERY_ORDER");
-  if (sc.fixed() || (e && std::atoi(e) == 0)) return;
+  if (sc.fixed() || (e && std::string(e) == "0")) return;
   h->entry_dist.ensure((size_t)nq * 4);
   h->order.ensure((size_t)nq * 4);
   GANN_HIP(gann::launch_query_order(h->ix, h->dtype, q_dev, nq, entries, h->entry_dist.as<float>(),
