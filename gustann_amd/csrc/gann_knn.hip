@@ -5,18 +5,20 @@
 //
 // One wavefront owns a block of queries and a slice of the base set and
 // scans it in tiles of 32 points.
-//  * uint8: 16 queries; the two 16x16 blocks of dot products of a tile come
-//    from v_mfma_i32_16x16x64_i8 on x - 128 and q - 128 (int8), so
+//  * uint8: the dot products come from int8 MFMA on x - 128 and q - 128, so
 //    ||q - x||^2 = |q'|^2 + |x'|^2 - 2 q'.x' is exact in int32 (at most
-//    256 * 255^2 < 2^24, exact again as float).  16 queries rather than 32
-//    halve the candidate buffers, so more wavefronts fit a CU's LDS.
+//    256 * 255^2 < 2^24, exact again as float).  Two forms (U8Form): 32
+//    queries with one 32x32 block of v_mfma_i32_32x32x32_i8 per tile, or 16
+//    queries with two 16x16 blocks of v_mfma_i32_16x16x64_i8, whose halved
+//    candidate buffers let more wavefronts fit a CU's LDS when k is large.
 //  * float: 32 queries; every lane forms 16 distances directly, sum over the
 //    dims in ascending order of fma(t, t, s), t = q - x.
 // A distance below the query's current k-th best is appended to the query's
 // LDS buffer; a buffer that could overflow with the next tile is cut back to
-// its k best by rank.  Points are scanned in increasing id order, so a tie
-// with the k-th best loses to it.  Each wavefront writes its sorted k best
-// per query; a tree of pairwise merges on the device folds the slices.
+// its k best (a merge of the new keys into the sorted kept ones).  Points are
+// scanned in increasing id order, so a tie with the k-th best loses to it.
+// Each wavefront writes its sorted k best per query; a tree of pairwise
+// merges on the device folds the slices.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
