@@ -563,10 +563,10 @@ int u8_blocks_per_cu(int dp, int k) {
 }  // namespace
 
 KnnU8Form knn_u8_form(int dim, int k) {
-  KnnU8Form f32{32, (dim + 31) / 32 * 32, 0}, f16{16, (dim + 63) / 64 * 64, 0};
-  f32.blocks_per_cu = u8_blocks_per_cu<32>(f32.dp, k);
-  f16.blocks_per_cu = u8_blocks_per_cu<16>(f16.dp, k);
-  return 16 * f16.blocks_per_cu > 32 * f32.blocks_per_cu ? f16 : f32;
+  KnnU8Form q32{32, (dim + 31) / 32 * 32, 0}, q16{16, (dim + 63) / 64 * 64, 0};
+  q32.blocks_per_cu = u8_blocks_per_cu<32>(q32.dp, k);
+  q16.blocks_per_cu = u8_blocks_per_cu<16>(q16.dp, k);
+  return 16 * q16.blocks_per_cu > 32 * q32.blocks_per_cu ? q16 : q32;
 }
 
 int knn_f32_blocks_per_cu(int dim, int k) {
